@@ -1,0 +1,289 @@
+"""ctypes binding of the C ABI in include/hllm_rocm.h (libhllm_rocm.so, built in-tree).
+
+There is no fallback: if the library is missing or fails to load, every entry point
+raises. ``Stage`` is a thin owner of one ``hllm_rocm_stage``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libhllm_rocm.so")
+ABI_VERSION = 1
+
+OK, INVALID_REQUEST, INCOMPATIBLE_WORKER, RESOURCE_EXHAUSTED = 0, 1, 2, 3
+DEADLINE_EXCEEDED, CANCELLED, INTERNAL = 4, 5, 6
+F32, F16, BF16 = 0, 1, 2
+ITEM_SAMPLE, ITEM_TOKEN_FROM_DEVICE, ITEM_LOGPROBS = 1, 2, 4
+STATUS_NAMES = {0: "OK", 1: "INVALID_REQUEST", 2: "INCOMPATIBLE_WORKER", 3: "RESOURCE_EXHAUSTED",
+                4: "DEADLINE_EXCEEDED", 5: "CANCELLED", 6: "INTERNAL"}
+EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_create",
+           "hllm_rocm_stage_destroy", "hllm_rocm_stage_load_tensor",
+           "hllm_rocm_stage_synthesize_tensor", "hllm_rocm_stage_finalize",
+           "hllm_rocm_stage_weight_memory", "hllm_rocm_stage_sequence_memory",
+           "hllm_rocm_sequence_allocate", "hllm_rocm_sequence_release",
+           "hllm_rocm_sequence_length", "hllm_rocm_stage_execute", "hllm_rocm_stage_submit",
+           "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
+           "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read")
+
+
+class StageError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class StageConfig(C.Structure):
+    _fields_ = [("abi_version", C.c_uint32), ("hidden_size", C.c_uint64),
+                ("intermediate_size", C.c_uint64), ("attention_heads", C.c_uint64),
+                ("key_value_heads", C.c_uint64), ("head_dimension", C.c_uint64),
+                ("maximum_sequence_length", C.c_uint64), ("vocabulary_size", C.c_uint64),
+                ("rms_norm_epsilon", C.c_float), ("rope_theta", C.c_float),
+                ("query_key_norm", C.c_uint32), ("layer_start", C.c_uint32),
+                ("layer_end", C.c_uint32), ("first_stage", C.c_uint32),
+                ("final_stage", C.c_uint32), ("tied_head", C.c_uint32),
+                ("execution_dtype", C.c_uint32), ("weight_dtype", C.c_uint32),
+                ("device", C.c_int32), ("kv_cache_bytes", C.c_uint64),
+                ("kv_block_tokens", C.c_uint32), ("max_sequences", C.c_uint32),
+                ("max_pass_rows", C.c_uint32)]
+
+
+class Item(C.Structure):
+    _fields_ = [("sequence", C.c_uint32), ("query_tokens", C.c_uint32),
+                ("first_position", C.c_uint64), ("flags", C.c_uint32),
+                ("top_logprobs", C.c_uint32), ("temperature", C.c_double),
+                ("top_p", C.c_double), ("top_k", C.c_uint64), ("seed", C.c_uint64),
+                ("generated_index", C.c_uint64)]
+
+
+class Pass(C.Structure):
+    _fields_ = [("items", C.c_uint32), ("item", C.POINTER(Item)),
+                ("token_ids", C.POINTER(C.c_uint64)), ("boundary_in", C.POINTER(C.c_uint16)),
+                ("cancelled", C.POINTER(C.c_int32)), ("tokens", C.POINTER(C.c_uint64)),
+                ("logprobs", C.POINTER(C.c_double)), ("top_ids", C.POINTER(C.c_uint64)),
+                ("top_logprobs", C.POINTER(C.c_double)),
+                ("boundary_out", C.POINTER(C.c_uint16)), ("logits", C.POINTER(C.c_float)),
+                ("trace_hidden", C.POINTER(C.c_float))]
+
+
+class Memory(C.Structure):
+    _fields_ = [("host_bytes", C.c_uint64), ("device_bytes", C.c_uint64),
+                ("pinned_host_bytes", C.c_uint64), ("unified_bytes", C.c_uint64)]
+
+
+_LIB = None
+
+
+def library() -> C.CDLL:
+    """Load libhllm_rocm.so; raises if it was not built (run hllm_amd/build.py)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIBRARY):
+        raise RuntimeError(f"{LIBRARY} is missing: build it with `python hllm_amd/build.py`")
+    L = C.CDLL(LIBRARY)
+    st, vp, u32, u64 = C.c_int, C.c_void_p, C.c_uint32, C.c_uint64
+    L.hllm_rocm_last_error.restype = C.c_char_p
+    L.hllm_rocm_abi_version.restype = u32
+    L.hllm_rocm_stage_create.argtypes = [C.POINTER(StageConfig), C.POINTER(vp)]
+    L.hllm_rocm_stage_destroy.argtypes = [vp]
+    L.hllm_rocm_stage_destroy.restype = None
+    L.hllm_rocm_stage_load_tensor.argtypes = [vp, C.c_char_p, u32, C.POINTER(u64), u32, vp, u64]
+    L.hllm_rocm_stage_synthesize_tensor.argtypes = [vp, C.c_char_p, u64, u64, C.c_float,
+                                                    C.c_float, u32]
+    L.hllm_rocm_stage_finalize.argtypes = [vp]
+    L.hllm_rocm_stage_weight_memory.argtypes = [vp, C.POINTER(Memory)]
+    L.hllm_rocm_stage_sequence_memory.argtypes = [vp, u64, u64, C.POINTER(Memory),
+                                                  C.POINTER(Memory)]
+    L.hllm_rocm_sequence_allocate.argtypes = [vp, u64, C.POINTER(u32)]
+    L.hllm_rocm_sequence_release.argtypes = [vp, u32]
+    L.hllm_rocm_sequence_length.argtypes = [vp, u32, C.POINTER(u64)]
+    L.hllm_rocm_stage_execute.argtypes = [vp, C.POINTER(Pass)]
+    L.hllm_rocm_stage_submit.argtypes = [vp, C.POINTER(Pass)]
+    L.hllm_rocm_stage_wait.argtypes = [vp]
+    L.hllm_rocm_stage_last_layout.argtypes = [vp, u32, u32, C.POINTER(C.c_int32),
+                                              C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
+    L.hllm_rocm_sequence_blocks.argtypes = [vp, u32, C.POINTER(C.c_int32), u32, C.POINTER(u32),
+                                            C.POINTER(u32)]
+    L.hllm_rocm_sequence_read_kv.argtypes = [vp, u32, u32, C.POINTER(C.c_float),
+                                             C.POINTER(C.c_float)]
+    L.hllm_rocm_stage_profile.argtypes = [vp, C.c_int32]
+    L.hllm_rocm_stage_profile_read.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double),
+                                               C.POINTER(u64), C.POINTER(u64)]
+    for name in EXPORTS:
+        fn = getattr(L, name)
+        if fn.restype is C.c_int or (fn.restype is None and name != "hllm_rocm_stage_destroy"):
+            fn.restype = st
+    if L.hllm_rocm_abi_version() != ABI_VERSION:
+        raise RuntimeError("libhllm_rocm.so ABI version mismatch")
+    _LIB = L
+    return L
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise StageError(status, library().hllm_rocm_last_error().decode())
+
+
+def _ptr(a, ctype):
+    return None if a is None else a.ctypes.data_as(C.POINTER(ctype))
+
+
+class Stage:
+    """One stage on one GPU (owner of an ``hllm_rocm_stage``)."""
+
+    def __init__(self, config: StageConfig):
+        self.lib = library()
+        self.config = config
+        handle = C.c_void_p()
+        check(self.lib.hllm_rocm_stage_create(C.byref(config), C.byref(handle)))
+        self.handle = handle
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.hllm_rocm_stage_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # --------------------------------------------------------------- weights
+    def load_tensor(self, name: str, array: np.ndarray, dtype: int | None = None) -> None:
+        a = np.ascontiguousarray(array)
+        if dtype is None:
+            dtype = {np.dtype(np.float32): F32, np.dtype(np.float16): F16,
+                     np.dtype(np.uint16): F16}[a.dtype]
+        shape = (C.c_uint64 * a.ndim)(*a.shape)
+        check(self.lib.hllm_rocm_stage_load_tensor(self.handle, name.encode(), dtype, shape, a.ndim,
+                                                   a.ctypes.data, a.nbytes))
+
+    def synthesize_tensor(self, name: str, seed: int, tensor_id: int, mean: float, sigma: float,
+                          source_dtype: int) -> None:
+        check(self.lib.hllm_rocm_stage_synthesize_tensor(self.handle, name.encode(), seed,
+                                                         tensor_id, mean, sigma, source_dtype))
+
+    def finalize(self) -> None:
+        check(self.lib.hllm_rocm_stage_finalize(self.handle))
+
+    def weight_memory(self) -> Memory:
+        m = Memory()
+        check(self.lib.hllm_rocm_stage_weight_memory(self.handle, C.byref(m)))
+        return m
+
+    def sequence_memory(self, tokens: int, max_query: int = 0):
+        cache, ws = Memory(), Memory()
+        check(self.lib.hllm_rocm_stage_sequence_memory(self.handle, tokens, max_query,
+                                                       C.byref(cache), C.byref(ws)))
+        return cache, ws
+
+    # --------------------------------------------------------------- sequences
+    def allocate(self, tokens: int) -> int:
+        h = C.c_uint32()
+        check(self.lib.hllm_rocm_sequence_allocate(self.handle, tokens, C.byref(h)))
+        return h.value
+
+    def release(self, sequence: int) -> None:
+        check(self.lib.hllm_rocm_sequence_release(self.handle, sequence))
+
+    def length(self, sequence: int) -> int:
+        n = C.c_uint64()
+        check(self.lib.hllm_rocm_sequence_length(self.handle, sequence, C.byref(n)))
+        return n.value
+
+    def blocks(self, sequence: int):
+        count, bt = C.c_uint32(), C.c_uint32()
+        check(self.lib.hllm_rocm_sequence_blocks(self.handle, sequence, None, 0, C.byref(count),
+                                                 C.byref(bt)))
+        out = np.zeros(count.value, np.int32)
+        check(self.lib.hllm_rocm_sequence_blocks(self.handle, sequence, _ptr(out, C.c_int32),
+                                                 count.value, C.byref(count), C.byref(bt)))
+        return out, bt.value
+
+    def read_kv(self, sequence: int, layer: int):
+        n = self.length(sequence)
+        c = self.config
+        k = np.zeros((n, c.key_value_heads, c.head_dimension), np.float32)
+        v = np.zeros_like(k)
+        check(self.lib.hllm_rocm_sequence_read_kv(self.handle, sequence, layer,
+                                                  _ptr(k, C.c_float), _ptr(v, C.c_float)))
+        return k, v
+
+    def last_layout(self, items: int, rows: int):
+        cu = np.zeros(items + 1, np.int32)
+        pos, slots = np.zeros(rows, np.int32), np.zeros(rows, np.int32)
+        check(self.lib.hllm_rocm_stage_last_layout(self.handle, items, rows, _ptr(cu, C.c_int32),
+                                                   _ptr(pos, C.c_int32), _ptr(slots, C.c_int32)))
+        return cu, pos, slots
+
+    # --------------------------------------------------------------- passes
+    def make_pass(self, items, token_ids=None, boundary=None, want_logits=False,
+                  trace=False, cancelled=None):
+        """Build a Pass (and the output arrays it points at) from a list of Item."""
+        n = len(items)
+        arr = (Item * n)(*items)
+        rows = sum(int(it.query_tokens) for it in items)
+        c = self.config
+        p = Pass()
+        p.items = n
+        p.item = arr
+        keep = {"items": arr}
+        if token_ids is not None:
+            ids = np.ascontiguousarray(token_ids, np.uint64)
+            keep["ids"] = ids
+            p.token_ids = _ptr(ids, C.c_uint64)
+        if boundary is not None:
+            b = np.ascontiguousarray(boundary, np.uint16)
+            keep["boundary"] = b
+            p.boundary_in = _ptr(b, C.c_uint16)
+        if cancelled is not None:
+            keep["cancelled"] = cancelled
+            p.cancelled = _ptr(cancelled, C.c_int32)
+        out = {"tokens": np.zeros(n, np.uint64)}
+        p.tokens = _ptr(out["tokens"], C.c_uint64)
+        if not c.final_stage:
+            out["boundary"] = np.zeros((rows, c.hidden_size), np.uint16)
+            p.boundary_out = _ptr(out["boundary"], C.c_uint16)
+        if want_logits and c.final_stage:
+            sampled = sum(1 for it in items if it.flags & ITEM_SAMPLE)
+            out["logits"] = np.zeros((sampled, c.vocabulary_size), np.float32)
+            p.logits = _ptr(out["logits"], C.c_float)
+        if trace:
+            out["trace"] = np.zeros((c.layer_end - c.layer_start, rows, c.hidden_size), np.float32)
+            p.trace_hidden = _ptr(out["trace"], C.c_float)
+        return p, out, keep
+
+    def execute(self, items, token_ids=None, boundary=None, want_logits=False, trace=False,
+                cancelled=None):
+        p, out, keep = self.make_pass(items, token_ids, boundary, want_logits, trace, cancelled)
+        check(self.lib.hllm_rocm_stage_execute(self.handle, C.byref(p)))
+        del keep
+        return out
+
+    # --------------------------------------------------------------- profiling
+    def profile(self, enable: bool) -> None:
+        check(self.lib.hllm_rocm_stage_profile(self.handle, int(enable)))
+
+    def profile_read(self, family: str):
+        ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
+        check(self.lib.hllm_rocm_stage_profile_read(self.handle, family.encode(), C.byref(ms),
+                                                    C.byref(n), C.byref(b)))
+        return ms.value, n.value, b.value
+
+
+def item(sequence: int, query_tokens: int, first_position: int, sample: bool = True,
+         from_device: bool = False, temperature: float = 0.0, top_p: float = 1.0, top_k: int = 0,
+         seed: int = 0, generated_index: int = 0, logprobs: bool = False,
+         top_logprobs: int = 0) -> Item:
+    flags = (ITEM_SAMPLE if sample else 0) | (ITEM_TOKEN_FROM_DEVICE if from_device else 0) | \
+        (ITEM_LOGPROBS if logprobs else 0)
+    return Item(sequence, query_tokens, first_position, flags, top_logprobs, temperature, top_p,
+                top_k, seed, generated_index)

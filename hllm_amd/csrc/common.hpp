@@ -1,0 +1,76 @@
+// Shared definitions for the gfx950 decoder stage worker.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "hllm_rocm.h"
+
+namespace hllm_rocm {
+
+// ------------------------------------------------------------------ errors
+
+// Mirrors runtime::Error (cpp/include/hllm/runtime/error.hpp:20-40): a category plus a
+// message; translated to hllm_status at the C ABI.
+struct Failure : std::runtime_error {
+  hllm_status status;
+  Failure(hllm_status s, const std::string& message) : std::runtime_error(message), status(s) {}
+};
+
+[[noreturn]] inline void fail(hllm_status s, const std::string& message) { throw Failure(s, message); }
+
+inline void check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  if (e == hipErrorOutOfMemory) fail(HLLM_RESOURCE_EXHAUSTED, std::string(what) + ": out of device memory");
+  fail(HLLM_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIP_CHECK(expr) ::hllm_rocm::check_hip((expr), #expr)
+
+// ------------------------------------------------------------------ vectors
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ F-layout
+//
+// Matrix operands of every GEMM live in a fragment-tiled layout sized for the
+// v_mfma_f32_16x16x32_f16 operand fragment: rows are padded to 16, columns to 32; each
+// 16x32 fragment is 1 KiB contiguous (fragments row-block-major), and inside a fragment
+// lane L = (r % 16) + 16 * ((c % 32) / 8) holds the 8 consecutive columns c..c+7 of row r.
+// A wave therefore loads one whole fragment with one coalesced 16-byte load per lane.
+__host__ __device__ inline uint64_t pad16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
+__host__ __device__ inline uint64_t pad32(uint64_t x) { return (x + 31) & ~uint64_t(31); }
+__host__ __device__ inline uint64_t flayout_index(uint64_t r, uint64_t c, uint64_t cols_padded) {
+  return (((((r >> 4) * (cols_padded >> 5) + (c >> 5)) << 6) + (r & 15) + ((c & 31) >> 3) * 16) << 3) +
+         (c & 7);
+}
+
+// Split F32 operands: x ~= hi + lo / 2048 with hi = f16(x), lo = f16((x - hi) * 2048).
+constexpr float kLoScale = 2048.0f;
+constexpr float kLoUnscale = 1.0f / 2048.0f;
+
+// ------------------------------------------------------------------ F16 (device)
+
+// Round-to-nearest-even F32 -> F16 with the reference codec's results for all finite and
+// infinite inputs (cpp/src/half.cpp:36-88); the hardware conversion rounds to nearest even.
+__device__ inline _Float16 to_half(float x) { return static_cast<_Float16>(x); }
+__device__ inline uint16_t half_bits(float x) {
+  _Float16 h = static_cast<_Float16>(x);
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ inline float from_half_bits(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// ------------------------------------------------------------------ precision
+
+// How GEMM operands are represented:
+//   1: f16 activations x f16 weights (F16 execution)
+//   2: split activations (hi + lo) x f16 weights (F32 execution over F16-resident weights)
+//   3: split activations x split weights (F32 execution over F32-resident weights)
+enum Precision : int { kF16 = 1, kSplitA = 2, kSplitAB = 3 };
+
+}  // namespace hllm_rocm

@@ -1,0 +1,40 @@
+// MFMA projections over F-layout operands (see gemm.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace hllm_rocm {
+
+enum Epilogue : int {
+  kEpiStore = 0,     // out[m][n] = y            (F32 row-major, leading dimension ldo)
+  kEpiResidual = 1,  // out[m][n] += y           (the F32 residual stream)
+  kEpiSwiglu = 2,    // F-layout act[m][i] = silu(gate) * up, gate/up in 32-wide interleaved groups
+};
+
+struct GemmArgs {
+  const uint16_t* w_hi;        // F-layout weights [N rows][Kp]
+  const uint16_t* w_lo;        // lo parts (F32 residency) or nullptr
+  const uint16_t* x_hi;        // F-layout activations [rows][Kp]
+  const uint16_t* x_lo;        // lo parts (F32 execution) or nullptr
+  int M;                       // rows, unless device_m is set
+  const int32_t* device_m;     // rows read on the device (sampled rows), <= the launch bound
+  int N;                       // output features
+  uint64_t Kp;                 // K padded to 32 (same for both operands)
+  int ksplit;                  // set by the launcher
+  float* workspace;            // split-K partial tiles
+  size_t workspace_floats;
+  int32_t* counters;           // per-tile arrival counters, zero between launches
+  int counter_count;
+  int epilogue;
+  float* out;                  // kEpiStore / kEpiResidual
+  int ldo;
+  uint16_t* out_hi;            // kEpiSwiglu
+  uint16_t* out_lo;
+  uint64_t out_cols_padded;
+};
+
+// Rows of the tile a launch with `rows_bound` rows uses (activation buffers are padded to it).
+int gemm_tile_rows(int rows_bound);
+void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus);
+
+}  // namespace hllm_rocm

@@ -1,0 +1,115 @@
+// Launchers for the stage's kernels. Every pointer is a device pointer unless named
+// `host_*`; every launch goes to `stream`.
+#pragma once
+
+#include "common.hpp"
+
+namespace hllm_rocm {
+
+// Per-item metadata uploaded for each pass (host packs, device unpacks).
+struct ItemMeta {
+  uint32_t sequence;       // sequence slot (block-table row)
+  uint32_t query_tokens;
+  uint32_t first_position;
+  uint32_t flags;          // HLLM_ITEM_*
+};
+
+// Where each packed row of a pass comes from, built on the device from ItemMeta.
+struct PackOut {
+  int32_t* cu_seqlens;     // [items + 1] exclusive prefix sum of query_tokens
+  int32_t* row_item;       // [rows]
+  int32_t* row_position;   // [rows]
+  int32_t* row_slot;       // [rows] physical KV slot: block * block_tokens + position % block_tokens
+  int32_t* row_token;      // [rows] input token (first stage)
+  int32_t* sample_row;     // [items] packed row of each sampling item, in item order (compacted)
+  int32_t* sample_item;    // [items]
+  int32_t* sample_count;   // [1]
+};
+
+struct KvView {
+  void* pool;              // [layers][blocks][2][kv_heads][block_tokens][head_dim]
+  uint64_t layer_stride;   // elements per layer
+  int32_t block_tokens;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t f32;             // element type: 1 = F32, 0 = F16
+};
+
+void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
+                 const int32_t* last_token, const int32_t* block_table, int table_width,
+                 int block_tokens, PackOut out);
+
+void launch_embed(hipStream_t stream, const uint16_t* table_hi, const uint16_t* table_lo,
+                  uint64_t cols_padded, const int32_t* row_token, int rows, int hidden, float* h);
+
+void launch_boundary_decode(hipStream_t stream, const uint16_t* in, int rows, int hidden, float* h);
+void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hidden, uint16_t* out,
+                            int32_t* flags);
+
+// y = (x * inv_rms) * w written to F-layout hi (+ lo when lo != nullptr); rows may be
+// gathered through `row_index` (nullptr = identity) with `count` read from device
+// memory when `device_rows` is non-null.
+void launch_rmsnorm_flayout(hipStream_t stream, const float* h, int hidden, const int32_t* row_index,
+                            int rows, const int32_t* device_rows, const float* weight, float eps,
+                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded);
+
+// Per-head QK-norm (optional) + rotate-half RoPE from tables + paged KV append. `qkv` is
+// [rows][(Q + 2K) * D] F32; q goes to `q_out` [rows][Q * D] F32.
+void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
+                            int head_dim, const float* q_norm, const float* k_norm, float eps,
+                            const float* rope_cos, const float* rope_sin, const int32_t* row_position,
+                            const int32_t* row_slot, KvView kv, int layer, float* q_out);
+
+// Split-context GQA attention for every packed row against its sequence's paged cache
+// (positions 0..row_position), then the split combine into F-layout A operands.
+struct AttentionArgs {
+  const float* q;              // [rows][Q][D]
+  int rows, q_heads, kv_heads, head_dim;
+  const int32_t* row_item;
+  const int32_t* row_position;
+  const ItemMeta* items;
+  const int32_t* block_table;
+  int table_width;
+  KvView kv;
+  int layer;
+  float scale;
+  float* partial;              // [rows][Q][max_splits][D + 2]
+  int max_splits;
+  int split_unit;              // positions per split are a multiple of this
+  uint16_t* out_hi;            // F-layout [rows][Q * D]
+  uint16_t* out_lo;
+  uint64_t out_cols_padded;
+};
+void launch_attention(hipStream_t stream, const AttentionArgs& a);
+
+// Row-wise first maximum over `cols` F32 values per row (greedy sampling) and a
+// non-finite flag (bit 1 of flags).
+void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
+                   int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
+                   int32_t* flags);
+
+// Record sampled tokens as the sequences' last tokens (for HLLM_ITEM_TOKEN_FROM_DEVICE).
+void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,
+                          const int32_t* sample_count, const ItemMeta* items, int32_t* last_token);
+
+// Weight relayout: row-major [rows][cols] source (F32/F16/BF16 payload, or the seeded
+// generator when `src == nullptr`) into F-layout hi (+ lo) at fused destination rows.
+struct RelayoutArgs {
+  const void* src;
+  uint32_t src_dtype;          // hllm_dtype
+  uint64_t seed, tensor_id;    // generator (src == nullptr)
+  float mean, sigma;
+  uint64_t rows, cols;         // this chunk's rows
+  uint64_t row_base;           // tensor row of the chunk's first row
+  uint16_t* dst_hi;
+  uint16_t* dst_lo;            // nullptr unless F32 residency
+  uint64_t dst_cols_padded;
+  int row_mode;                // 0: dst_row = row_offset + r; 1: interleave 32-row blocks (gate); 2: (up)
+  uint64_t row_offset;
+  float* dst_f32;              // vectors (norm weights): F32 copy instead of F-layout
+  int f16_resident;            // weights are held as F16 (vectors: rounded through F16)
+  int32_t* flags;              // bit 0: non-finite source value, bit 2: not finite in F16
+};
+void launch_relayout(hipStream_t stream, const RelayoutArgs& a);
+
+}  // namespace hllm_rocm

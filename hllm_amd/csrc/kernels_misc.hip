@@ -1,0 +1,470 @@
+// Bandwidth-light kernels of a pass: ragged packing, embedding gather, F16 boundary
+// codec, RMSNorm into GEMM operands, QK-norm + RoPE + paged KV append, greedy argmax,
+// and checkpoint relayout. All are memory- or latency-bound; none reshapes work into GEMMs.
+#include "kernels.hpp"
+
+namespace hllm_rocm {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ inline float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ inline int wave_sum_int(int v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over a 256-thread block in a fixed order (deterministic).
+__device__ inline float block_sum(float v, float* scratch) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) total += scratch[w];
+  __syncthreads();
+  return total;
+}
+
+// ------------------------------------------------------------------ packing
+
+// One block per item: its row offset and sampling rank are prefix sums over the items
+// before it (item order = scheduler claim order).
+__global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int n_items,
+                                                     const int32_t* host_tokens,
+                                                     const int32_t* last_token,
+                                                     const int32_t* block_table, int table_width,
+                                                     int block_tokens, PackOut out) {
+  __shared__ int scratch[8];
+  const int i = blockIdx.x;
+  int offset = 0, samples = 0;
+  for (int j = threadIdx.x; j < i; j += blockDim.x) {
+    offset += (int)items[j].query_tokens;
+    samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
+  }
+  offset = wave_sum_int(offset);
+  samples = wave_sum_int(samples);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    scratch[wave] = offset;
+    scratch[4 + wave] = samples;
+  }
+  __syncthreads();
+  offset = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+  samples = scratch[4] + scratch[5] + scratch[6] + scratch[7];
+  const ItemMeta it = items[i];
+  const bool sample = (it.flags & HLLM_ITEM_SAMPLE) != 0;
+  if (threadIdx.x == 0) {
+    out.cu_seqlens[i] = offset;
+    if (sample) {
+      out.sample_row[samples] = offset + (int)it.query_tokens - 1;
+      out.sample_item[samples] = i;
+    }
+    if (i == n_items - 1) {
+      out.cu_seqlens[n_items] = offset + (int)it.query_tokens;
+      *out.sample_count = samples + (sample ? 1 : 0);
+    }
+  }
+  const int32_t* table = block_table + (size_t)it.sequence * table_width;
+  for (int j = threadIdx.x; j < (int)it.query_tokens; j += blockDim.x) {
+    const int r = offset + j;
+    const int position = (int)it.first_position + j;
+    out.row_item[r] = i;
+    out.row_position[r] = position;
+    out.row_slot[r] = table[position / block_tokens] * block_tokens + position % block_tokens;
+    out.row_token[r] = (it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) ? last_token[it.sequence]
+                                                                 : host_tokens[r];
+  }
+}
+
+// ------------------------------------------------------------------ embedding / boundary
+
+__global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* hi, const uint16_t* lo,
+                                                      uint64_t cols_padded,
+                                                      const int32_t* row_token, int hidden,
+                                                      float* h) {
+  const int r = blockIdx.x;
+  const uint64_t id = (uint64_t)row_token[r];
+  float* out = h + (size_t)r * hidden;
+  for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
+    const uint64_t at = flayout_index(id, c, cols_padded);
+    const half8 vh = *reinterpret_cast<const half8*>(hi + at);
+    half8 vl = {};
+    if (lo) vl = *reinterpret_cast<const half8*>(lo + at);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c + j < hidden) out[c + j] = (float)vh[j] + (float)vl[j] * kLoUnscale;
+    }
+  }
+}
+
+__global__ void boundary_decode_kernel(const uint16_t* in, uint64_t n, float* h) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) h[i] = from_half_bits(in[i]);
+}
+
+__global__ void boundary_encode_kernel(const float* h, uint64_t n, uint16_t* out, int32_t* flags) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint16_t b = half_bits(h[i]);
+  out[i] = b;
+  if ((b & 0x7c00u) == 0x7c00u) atomicOr(flags, 4);
+}
+
+// ------------------------------------------------------------------ RMSNorm -> operand
+
+__global__ void __launch_bounds__(kBlock) rmsnorm_flayout_kernel(
+    const float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
+    const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
+  __shared__ float scratch[4];
+  const int r = blockIdx.x;
+  const int count = device_rows ? *device_rows : rows;
+  if (r >= count) return;
+  const int src = row_index ? row_index[r] : r;
+  const float* x = h + (size_t)src * hidden;
+  float squares = 0.0f;
+  for (int c = threadIdx.x; c < hidden; c += blockDim.x) squares += x[c] * x[c];
+  squares = block_sum(squares, scratch);
+  const float inverse = 1.0f / sqrtf(squares / (float)hidden + eps);
+  for (int c0 = threadIdx.x * 8; c0 < (int)cols_padded; c0 += blockDim.x * 8) {
+    half8 vh, vl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + j;
+      const float y = c < hidden ? (x[c] * inverse) * weight[c] : 0.0f;
+      vh[j] = to_half(y);
+      vl[j] = to_half((y - (float)vh[j]) * kLoScale);
+    }
+    const uint64_t at = flayout_index(r, c0, cols_padded);
+    *reinterpret_cast<half8*>(out_hi + at) = vh;
+    if (out_lo) *reinterpret_cast<half8*>(out_lo + at) = vl;
+  }
+}
+
+// ------------------------------------------------------------------ QK-norm + RoPE + KV append
+
+__device__ inline uint64_t kv_index(const KvView& kv, int layer, int slot, int which, int head,
+                                    int d) {
+  const int block = slot / kv.block_tokens;
+  const int offset = slot - block * kv.block_tokens;
+  return (uint64_t)layer * kv.layer_stride +
+         (((uint64_t)block * 2 + which) * kv.kv_heads + head) * (uint64_t)kv.block_tokens *
+             kv.head_dim +
+         (uint64_t)offset * kv.head_dim + d;
+}
+
+// One wave per head. Lane l holds elements d = l + 64 j. Head dimensions are powers of two
+// in [4, 256]: for D >= 128 both members of a rotate-half pair (d, d + D/2) sit in the same
+// lane; for D <= 64 the partner is lane l ^ (D/2).
+__global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
+    const float* qkv, int q_heads, int kv_heads, int head_dim, const float* q_norm,
+    const float* k_norm, float eps, const float* rope_cos, const float* rope_sin,
+    const int32_t* row_position, const int32_t* row_slot, KvView kv, int layer, float* q_out) {
+  const int r = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
+  const int heads = q_heads + 2 * kv_heads;
+  const int D = head_dim, half = D / 2;
+  const int per_lane = D >= 64 ? D / 64 : 1;
+  const int position = row_position[r];
+  const int slot = row_slot[r];
+  const float* row = qkv + (size_t)r * heads * D;
+  const float* cos_row = rope_cos + (size_t)position * half;
+  const float* sin_row = rope_sin + (size_t)position * half;
+  for (int head = wave; head < heads; head += waves) {
+    const bool is_q = head < q_heads;
+    const bool is_v = head >= q_heads + kv_heads;
+    const float* src = row + head * D;
+    float v[4];
+    float squares = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = lane + 64 * j;
+      v[j] = (j < per_lane && d < D) ? src[d] : 0.0f;
+      squares += v[j] * v[j];
+    }
+    if (!is_v) {
+      const float* w = is_q ? q_norm : k_norm;
+      if (w) {
+        squares = wave_sum(squares);
+        const float inverse = 1.0f / sqrtf(squares / (float)D + eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = lane + 64 * j;
+          if (j < per_lane && d < D) v[j] = v[j] * (inverse * w[d]);
+        }
+      }
+      if (D >= 128) {
+        const int pairs = per_lane / 2;  // elements [0, pairs) are first halves
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (j < pairs) {
+            const int d = lane + 64 * j;
+            const float c = cos_row[d], s = sin_row[d];
+            const float a = v[j], b = v[j + pairs];
+            v[j] = a * c - b * s;
+            v[j + pairs] = b * c + a * s;
+          }
+        }
+      } else {
+        const float partner = __shfl_xor(v[0], half, 64);
+        if (lane < D) {
+          if (lane < half) {
+            const float c = cos_row[lane], s = sin_row[lane];
+            v[0] = v[0] * c - partner * s;
+          } else {
+            const float c = cos_row[lane - half], s = sin_row[lane - half];
+            v[0] = v[0] * c + partner * s;
+          }
+        }
+      }
+    }
+    if (is_q) {
+      float* dst = q_out + ((size_t)r * q_heads + head) * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (j < per_lane && d < D) dst[d] = v[j];
+      }
+    } else {
+      const int which = is_v ? 1 : 0;
+      const int kvh = head - q_heads - (is_v ? kv_heads : 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (j < per_lane && d < D) {
+          const uint64_t at = kv_index(kv, layer, slot, which, kvh, d);
+          if (kv.f32)
+            static_cast<float*>(kv.pool)[at] = v[j];
+          else
+            static_cast<_Float16*>(kv.pool)[at] = to_half(v[j]);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ greedy argmax
+
+struct Best {
+  float value;
+  int index;
+};
+__device__ inline Best better(Best a, Best b) {
+  // First maximum: larger value wins; equal values keep the lower index.
+  if (b.value > a.value || (b.value == a.value && b.index < a.index)) return b;
+  return a;
+}
+__device__ inline Best wave_best(Best x) {
+  for (int o = 32; o > 0; o >>= 1) {
+    Best y{__shfl_xor(x.value, o, 64), __shfl_xor(x.index, o, 64)};
+    x = better(x, y);
+  }
+  return x;
+}
+
+__global__ void __launch_bounds__(kBlock) argmax_partial_kernel(const float* logits,
+                                                               const int32_t* device_rows, int cols,
+                                                               int parts, float* part_val,
+                                                               int32_t* part_idx, int32_t* flags) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int r = blockIdx.x, part = blockIdx.y;
+  if (r >= *device_rows) return;
+  const int chunk = (cols + parts - 1) / parts;
+  const int c0 = part * chunk, c1 = min(cols, c0 + chunk);
+  const float* row = logits + (size_t)r * cols;
+  Best best{-INFINITY, 0x7fffffff};
+  bool bad = false;
+  for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
+    const float x = row[c];
+    bad |= !isfinite(x);
+    best = better(best, Best{x, c});
+  }
+  if (bad) atomicOr(flags, 2);
+  best = wave_best(best);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best.value;
+    si[wave] = best.index;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Best b{sv[0], si[0]};
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) b = better(b, Best{sv[w], si[w]});
+    part_val[(size_t)r * parts + part] = b.value;
+    part_idx[(size_t)r * parts + part] = b.index;
+  }
+}
+
+__global__ void argmax_final_kernel(const int32_t* device_rows, int parts, const float* part_val,
+                                    const int32_t* part_idx, int32_t* tokens) {
+  const int r = blockIdx.x;
+  if (r >= *device_rows) return;
+  Best best{-INFINITY, 0x7fffffff};
+  for (int p = threadIdx.x; p < parts; p += 64) {
+    best = better(best, Best{part_val[(size_t)r * parts + p], part_idx[(size_t)r * parts + p]});
+  }
+  best = wave_best(best);
+  if (threadIdx.x == 0) tokens[r] = best.index == 0x7fffffff ? 0 : best.index;
+}
+
+__global__ void record_tokens_kernel(const int32_t* tokens, const int32_t* sample_item,
+                                     const int32_t* sample_count, const ItemMeta* items,
+                                     int32_t* last_token) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < *sample_count) last_token[items[sample_item[j]].sequence] = tokens[j];
+}
+
+// ------------------------------------------------------------------ checkpoint relayout
+
+__device__ inline uint64_t splitmix64(uint64_t state) {
+  uint64_t z = state + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// Irwin-Hall(12) approximation of N(0,1) from a counter-based SplitMix64 stream, then
+// mean + n * sigma with one rounding per operation (no fused multiply-add).
+__device__ inline float synth_value(uint64_t seed, uint64_t tensor_id, uint64_t index, float mean,
+                                    float sigma) {
+  const uint64_t base = (tensor_id << 40) + 3ull * index;
+  int sum = 0;
+#pragma unroll
+  for (uint64_t j = 0; j < 3; ++j) {
+    const uint64_t bits = splitmix64(seed + 0x9e3779b97f4a7c15ull * (base + j));
+    sum += (int)(bits & 0xffffu) + (int)((bits >> 16) & 0xffffu) + (int)((bits >> 32) & 0xffffu) +
+           (int)(bits >> 48);
+  }
+  const float n = (float)(sum + 6 - 6 * 65536) * (1.0f / 65536.0f);
+  return __fadd_rn(mean, __fmul_rn(n, sigma));
+}
+
+__device__ inline float source_value(const RelayoutArgs& a, uint64_t r, uint64_t c) {
+  const uint64_t i = r * a.cols + c;
+  if (!a.src) {
+    const float v = synth_value(a.seed, a.tensor_id, (a.row_base + r) * a.cols + c, a.mean, a.sigma);
+    return a.src_dtype == HLLM_DTYPE_F16 ? (float)to_half(v) : v;
+  }
+  switch (a.src_dtype) {
+    case HLLM_DTYPE_F32:
+      return static_cast<const float*>(a.src)[i];
+    case HLLM_DTYPE_F16:
+      return from_half_bits(static_cast<const uint16_t*>(a.src)[i]);
+    default: {
+      const uint32_t w = (uint32_t) static_cast<const uint16_t*>(a.src)[i] << 16;
+      return __builtin_bit_cast(float, w);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) relayout_kernel(RelayoutArgs a) {
+  const uint64_t chunks_per_row = (a.cols + 7) / 8;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.rows * chunks_per_row) return;
+  const uint64_t r = t / chunks_per_row;
+  const uint64_t c0 = (t - r * chunks_per_row) * 8;
+  int bad = 0;
+  if (a.dst_f32) {  // vector weights keep F32 storage of the resident value
+    for (uint64_t c = c0; c < c0 + 8 && c < a.cols; ++c) {
+      float v = source_value(a, r, c);
+      if (!isfinite(v)) bad |= 1;
+      if (a.f16_resident) {
+        const _Float16 h = to_half(v);
+        if (!isfinite((float)h)) bad |= 4;
+        v = (float)h;
+      }
+      a.dst_f32[(a.row_base + r) * a.cols + c] = v;
+    }
+  } else {
+    const uint64_t tr = a.row_base + r;
+    uint64_t dr = a.row_offset + tr;
+    if (a.row_mode == 1) dr = a.row_offset + (tr / 32) * 64 + (tr % 32);
+    if (a.row_mode == 2) dr = a.row_offset + (tr / 32) * 64 + 32 + (tr % 32);
+    half8 vh = {}, vl = {};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c0 + j < a.cols) {
+        const float v = source_value(a, r, c0 + j);
+        if (!isfinite(v)) bad |= 1;
+        vh[j] = to_half(v);
+        if (a.f16_resident && !isfinite((float)vh[j])) bad |= 4;
+        vl[j] = to_half((v - (float)vh[j]) * kLoScale);
+      }
+    }
+    const uint64_t at = flayout_index(dr, c0, a.dst_cols_padded);
+    *reinterpret_cast<half8*>(a.dst_hi + at) = vh;
+    if (a.dst_lo) *reinterpret_cast<half8*>(a.dst_lo + at) = vl;
+  }
+  if (bad) atomicOr(a.flags, bad);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+
+void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
+                 const int32_t* last_token, const int32_t* block_table, int table_width,
+                 int block_tokens, PackOut out) {
+  pack_kernel<<<n_items, kBlock, 0, stream>>>(items, n_items, host_tokens, last_token, block_table,
+                                               table_width, block_tokens, out);
+}
+
+void launch_embed(hipStream_t stream, const uint16_t* table_hi, const uint16_t* table_lo,
+                  uint64_t cols_padded, const int32_t* row_token, int rows, int hidden, float* h) {
+  embed_kernel<<<rows, kBlock, 0, stream>>>(table_hi, table_lo, cols_padded, row_token, hidden, h);
+}
+
+void launch_boundary_decode(hipStream_t stream, const uint16_t* in, int rows, int hidden, float* h) {
+  const uint64_t n = (uint64_t)rows * hidden;
+  boundary_decode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(in, n, h);
+}
+
+void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hidden, uint16_t* out,
+                            int32_t* flags) {
+  const uint64_t n = (uint64_t)rows * hidden;
+  boundary_encode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(h, n, out,
+                                                                                      flags);
+}
+
+void launch_rmsnorm_flayout(hipStream_t stream, const float* h, int hidden, const int32_t* row_index,
+                            int rows, const int32_t* device_rows, const float* weight, float eps,
+                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
+  if (rows <= 0) return;
+  rmsnorm_flayout_kernel<<<rows, kBlock, 0, stream>>>(h, hidden, row_index, rows, device_rows,
+                                                      weight, eps, out_hi, out_lo, cols_padded);
+}
+
+void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
+                            int head_dim, const float* q_norm, const float* k_norm, float eps,
+                            const float* rope_cos, const float* rope_sin, const int32_t* row_position,
+                            const int32_t* row_slot, KvView kv, int layer, float* q_out) {
+  qkv_rope_append_kernel<<<rows, kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
+                                                      k_norm, eps, rope_cos, rope_sin, row_position,
+                                                      row_slot, kv, layer, q_out);
+}
+
+void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
+                   int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
+                   int32_t* flags) {
+  if (max_rows <= 0) return;
+  argmax_partial_kernel<<<dim3(max_rows, parts), kBlock, 0, stream>>>(logits, device_rows, cols,
+                                                                      parts, part_val, part_idx,
+                                                                      flags);
+  argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens);
+}
+
+void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,
+                          const int32_t* sample_count, const ItemMeta* items, int32_t* last_token) {
+  record_tokens_kernel<<<8, 128, 0, stream>>>(tokens, sample_item, sample_count, items, last_token);
+}
+
+void launch_relayout(hipStream_t stream, const RelayoutArgs& a) {
+  const uint64_t threads = a.rows * ((a.cols + 7) / 8);
+  relayout_kernel<<<(unsigned)((threads + kBlock - 1) / kBlock), kBlock, 0, stream>>>(a);
+}
+
+}  // namespace hllm_rocm

@@ -1,0 +1,1126 @@
+// The stage runtime behind the C ABI: weights resident in HBM in the F-layout, a paged KV
+// pool with a host-side block allocator, per-pass workspaces reserved up front, and the
+// pass pipeline (pack -> embed/decode -> layers -> head/argmax or boundary encode).
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "gemm.hpp"
+#include "kernels.hpp"
+
+namespace hllm_rocm {
+namespace {
+
+thread_local std::string g_last_error;
+
+uint64_t pad_to(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
+
+// Device allocation owned by the stage (RAII: a failed construction frees what it got).
+struct DeviceMemory {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceMemory() = default;
+  DeviceMemory(const DeviceMemory&) = delete;
+  DeviceMemory& operator=(const DeviceMemory&) = delete;
+  ~DeviceMemory() {
+    if (ptr) (void)hipFree(ptr);
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  void allocate(size_t n, const char* what) {
+    bytes = n;
+    if (n == 0) return;
+    const hipError_t e = hipMalloc(&ptr, n);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      fail(HLLM_RESOURCE_EXHAUSTED, std::string("device allocation failed: ") + what + " (" +
+                                        std::to_string(n) + " bytes)");
+    }
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+struct PinnedMemory {
+  void* ptr = nullptr;
+  PinnedMemory() = default;
+  PinnedMemory(const PinnedMemory&) = delete;
+  PinnedMemory& operator=(const PinnedMemory&) = delete;
+  ~PinnedMemory() {
+    if (ptr) (void)hipHostFree(ptr);
+  }
+  void allocate(size_t n) { HIP_CHECK(hipHostMalloc(&ptr, n == 0 ? 1 : n, hipHostMallocDefault)); }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+struct Matrix {  // an F-layout weight: hi parts and optional lo parts
+  DeviceMemory hi, lo;
+  uint64_t rows_padded = 0, cols_padded = 0;
+};
+
+struct Layer {
+  Matrix qkv, o, gate_up, down;
+  DeviceMemory input_norm, post_norm, q_norm, k_norm;
+};
+
+struct Sequence {
+  bool live = false;
+  bool failed = false;
+  uint64_t capacity = 0;
+  uint64_t length = 0;
+  std::vector<int32_t> blocks;
+};
+
+// Expected tensor: shape and where it goes.
+struct Target {
+  std::vector<uint64_t> shape;
+  Matrix* matrix = nullptr;
+  DeviceMemory* vector = nullptr;
+  int row_mode = 0;
+  uint64_t row_offset = 0;
+  bool loaded = false;
+};
+
+struct Profile {
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+  uint64_t bytes = 0;
+};
+
+constexpr int kMaxSplits = 16;
+constexpr int kSplitUnit = 256;
+constexpr int kArgmaxParts = 64;
+constexpr uint64_t kStagingBytes = 64ull << 20;
+
+}  // namespace
+
+class Stage {
+ public:
+  explicit Stage(const hllm_rocm_stage_config& c);
+  ~Stage();
+  void load_tensor(const std::string& name, uint32_t dtype, const uint64_t* shape, uint32_t rank,
+                   const void* data, uint64_t bytes);
+  void synthesize(const std::string& name, uint64_t seed, uint64_t tensor_id, float mean, float sigma,
+                  uint32_t source_dtype);
+  void finalize();
+  hllm_rocm_memory weight_memory() const { return {0, weight_bytes_, 0, 0}; }
+  void sequence_memory(uint64_t tokens, uint64_t max_query, hllm_rocm_memory* cache,
+                       hllm_rocm_memory* workspace) const;
+  uint32_t allocate_sequence(uint64_t tokens);
+  void release_sequence(uint32_t handle);
+  uint64_t sequence_length(uint32_t handle) const;
+  void submit(const hllm_rocm_pass& pass);
+  void wait();
+  void last_layout(uint32_t items, uint32_t rows, int32_t* cu, int32_t* pos, int32_t* slots);
+  void sequence_blocks(uint32_t handle, int32_t* blocks, uint32_t capacity, uint32_t* count,
+                       uint32_t* block_tokens);
+  void read_kv(uint32_t handle, uint32_t layer, float* keys, float* values);
+  void set_profiling(bool on);
+  void profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes);
+
+ private:
+  void check_sizes();
+  Target& target(const std::string& name);
+  void relayout(Target& t, const std::string& name, const void* device_src, uint32_t dtype,
+                uint64_t seed, uint64_t tensor_id, float mean, float sigma, uint64_t row_base,
+                uint64_t rows);
+  void read_flags(const char* context);
+  void gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo, int rows,
+            int n, int epilogue, float* out, int ldo, uint16_t* out_hi, uint16_t* out_lo,
+            uint64_t out_cols_padded);
+  template <typename F>
+  void timed(const char* family, uint64_t bytes, F&& launch);
+  void fail_pass(const std::vector<uint32_t>& sequences);
+
+  hllm_rocm_stage_config c_;
+  int device_ = 0;
+  int cus_ = 256;
+  hipStream_t stream_ = nullptr;
+  int prec_ = kF16;
+  bool kv_f32_ = false;
+  bool w_f32_ = false;
+  uint64_t H_, I_, Q_, K_, D_, V_, L_, Hp_, Ip_, QDp_, qkv_n_;
+  uint64_t rows_max_, rows_padded_, items_max_;
+  uint64_t weight_bytes_ = 0;
+  bool finalized_ = false;
+
+  std::vector<std::unique_ptr<Layer>> layers_;
+  Matrix embedding_, head_;
+  DeviceMemory final_norm_;
+  std::map<std::string, Target> targets_;
+  DeviceMemory rope_cos_, rope_sin_;
+
+  // paged KV
+  DeviceMemory kv_pool_;
+  KvView kv_{};
+  uint64_t blocks_total_ = 0;
+  int table_width_ = 0;
+  std::vector<int32_t> free_blocks_;
+  std::vector<Sequence> sequences_;
+  std::vector<uint32_t> free_slots_;
+  DeviceMemory block_table_, last_token_;
+  mutable std::mutex seq_mutex_;
+  std::mutex pass_mutex_;
+
+  // workspaces
+  DeviceMemory h_, a0_hi_, a0_lo_, a1_hi_, a1_lo_, qkv_, q_, attn_partial_;
+  DeviceMemory gemm_ws_, gemm_counters_, logits_, argmax_val_, argmax_idx_, tokens_, flags_;
+  DeviceMemory items_dev_, host_tokens_dev_, pack_buf_, boundary_dev_, staging_;
+  size_t gemm_ws_floats_ = 0;
+  int gemm_counter_count_ = 0;
+  PackOut pack_{};
+  PinnedMemory pin_items_, pin_tokens_, pin_out_tokens_, pin_flags_, pin_boundary_;
+
+  // in-flight pass
+  bool in_flight_ = false;
+  hllm_rocm_pass pending_{};
+  std::vector<uint32_t> pending_sequences_;
+  std::vector<uint32_t> pending_lengths_;
+  std::vector<int> pending_sample_items_;
+  uint64_t pending_rows_ = 0;
+
+  bool profiling_ = false;
+  std::map<std::string, Profile> profiles_;
+  std::vector<hipEvent_t> event_pool_;
+};
+
+// --------------------------------------------------------------------- construction
+
+Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
+  if (c.abi_version != HLLM_ROCM_ABI_VERSION) fail(HLLM_INCOMPATIBLE_WORKER, "ABI version mismatch");
+  check_sizes();
+  device_ = c.device;
+  HIP_CHECK(hipSetDevice(device_));
+  HIP_CHECK(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, device_));
+  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+
+  H_ = c.hidden_size;
+  I_ = c.intermediate_size;
+  Q_ = c.attention_heads;
+  K_ = c.key_value_heads;
+  D_ = c.head_dimension;
+  V_ = c.vocabulary_size;
+  L_ = c.layer_end - c.layer_start;
+  Hp_ = pad32(H_);
+  Ip_ = pad32(I_);
+  QDp_ = pad32(Q_ * D_);
+  qkv_n_ = (Q_ + 2 * K_) * D_;
+  const bool f32_exec = c.execution_dtype == HLLM_DTYPE_F32;
+  w_f32_ = c.weight_dtype == HLLM_DTYPE_F32;
+  prec_ = !f32_exec ? kF16 : (w_f32_ ? kSplitAB : kSplitA);
+  kv_f32_ = f32_exec;
+  rows_max_ = c.max_pass_rows ? c.max_pass_rows : 2048;
+  rows_padded_ = pad_to(rows_max_, 128);
+  const uint64_t seq_max = c.max_sequences ? c.max_sequences : 512;
+  items_max_ = std::min<uint64_t>(std::max<uint64_t>(seq_max, 1), 1024);
+  const int bt = c.kv_block_tokens ? (int)c.kv_block_tokens : 64;
+
+  // ---- weights
+  const size_t wel = w_f32_ ? 2 : 1;  // hi (+ lo) parts
+  auto matrix = [&](Matrix& m, uint64_t rows, uint64_t cols, const char* what) {
+    m.rows_padded = pad_to(rows, 128);
+    m.cols_padded = pad32(cols);
+    const size_t bytes = m.rows_padded * m.cols_padded * 2;
+    m.hi.allocate(bytes, what);
+    HIP_CHECK(hipMemsetAsync(m.hi.ptr, 0, bytes, stream_));
+    if (w_f32_) {
+      m.lo.allocate(bytes, what);
+      HIP_CHECK(hipMemsetAsync(m.lo.ptr, 0, bytes, stream_));
+    }
+    weight_bytes_ += rows * cols * 2 * wel;
+  };
+  auto vec = [&](DeviceMemory& v, uint64_t n, const char* what) {
+    v.allocate(n * sizeof(float), what);
+    weight_bytes_ += n * 2 * wel;
+  };
+  const std::string root = "model.layers.";
+  for (uint64_t i = 0; i < L_; ++i) {
+    layers_.push_back(std::make_unique<Layer>());
+    Layer& l = *layers_.back();
+    const std::string p = root + std::to_string(c.layer_start + i) + ".";
+    matrix(l.qkv, qkv_n_, H_, "qkv");
+    matrix(l.o, H_, Q_ * D_, "o_proj");
+    matrix(l.gate_up, 2 * Ip_, H_, "gate_up");
+    matrix(l.down, H_, Ip_, "down_proj");
+    weight_bytes_ -= (2 * Ip_ - 2 * I_) * H_ * 2 * wel + H_ * (Ip_ - I_) * 2 * wel;
+    vec(l.input_norm, H_, "norm");
+    vec(l.post_norm, H_, "norm");
+    targets_[p + "input_layernorm.weight"] = {{H_}, nullptr, &l.input_norm};
+    targets_[p + "post_attention_layernorm.weight"] = {{H_}, nullptr, &l.post_norm};
+    targets_[p + "self_attn.q_proj.weight"] = {{Q_ * D_, H_}, &l.qkv, nullptr, 0, 0};
+    targets_[p + "self_attn.k_proj.weight"] = {{K_ * D_, H_}, &l.qkv, nullptr, 0, Q_ * D_};
+    targets_[p + "self_attn.v_proj.weight"] = {{K_ * D_, H_}, &l.qkv, nullptr, 0, (Q_ + K_) * D_};
+    targets_[p + "self_attn.o_proj.weight"] = {{H_, Q_ * D_}, &l.o, nullptr, 0, 0};
+    targets_[p + "mlp.gate_proj.weight"] = {{I_, H_}, &l.gate_up, nullptr, 1, 0};
+    targets_[p + "mlp.up_proj.weight"] = {{I_, H_}, &l.gate_up, nullptr, 2, 0};
+    targets_[p + "mlp.down_proj.weight"] = {{H_, I_}, &l.down, nullptr, 0, 0};
+    if (c.query_key_norm) {
+      vec(l.q_norm, D_, "qk_norm");
+      vec(l.k_norm, D_, "qk_norm");
+      targets_[p + "self_attn.q_norm.weight"] = {{D_}, nullptr, &l.q_norm};
+      targets_[p + "self_attn.k_norm.weight"] = {{D_}, nullptr, &l.k_norm};
+    }
+  }
+  if (c.first_stage || (c.final_stage && c.tied_head)) {
+    matrix(embedding_, V_, H_, "embedding");
+    targets_["model.embed_tokens.weight"] = {{V_, H_}, &embedding_, nullptr, 0, 0};
+  }
+  if (c.final_stage) {
+    vec(final_norm_, H_, "final_norm");
+    targets_["model.norm.weight"] = {{H_}, nullptr, &final_norm_};
+    if (!c.tied_head) {
+      matrix(head_, V_, H_, "lm_head");
+      targets_["lm_head.weight"] = {{V_, H_}, &head_, nullptr, 0, 0};
+    }
+  }
+
+  // ---- RoPE tables, computed on the host with the CPU worker's float calls
+  // (angle = position / powf(theta, 2i / D), cosf, sinf: cpp/src/cpu/llama.cpp:222-231).
+  {
+    const uint64_t half = D_ / 2, positions = c.maximum_sequence_length;
+    std::vector<float> denominators(half), cs(positions * half), sn(positions * half);
+    for (uint64_t i = 0; i < half; ++i) {
+      denominators[i] = std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D_));
+    }
+    for (uint64_t p = 0; p < positions; ++p) {
+      for (uint64_t i = 0; i < half; ++i) {
+        const float angle = static_cast<float>(p) / denominators[i];
+        cs[p * half + i] = std::cos(angle);
+        sn[p * half + i] = std::sin(angle);
+      }
+    }
+    rope_cos_.allocate(cs.size() * sizeof(float), "rope");
+    rope_sin_.allocate(sn.size() * sizeof(float), "rope");
+    HIP_CHECK(hipMemcpy(rope_cos_.ptr, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(rope_sin_.ptr, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+
+  // ---- workspaces
+  const size_t R = rows_padded_;
+  h_.allocate(R * H_ * sizeof(float), "hidden");
+  const uint64_t a0_cols = Hp_, a1_cols = std::max(QDp_, Ip_);
+  a0_hi_.allocate(R * a0_cols * 2, "operand");
+  a1_hi_.allocate(R * a1_cols * 2, "operand");
+  HIP_CHECK(hipMemsetAsync(a0_hi_.ptr, 0, a0_hi_.bytes, stream_));
+  HIP_CHECK(hipMemsetAsync(a1_hi_.ptr, 0, a1_hi_.bytes, stream_));
+  if (prec_ >= kSplitA) {
+    a0_lo_.allocate(R * a0_cols * 2, "operand");
+    a1_lo_.allocate(R * a1_cols * 2, "operand");
+    HIP_CHECK(hipMemsetAsync(a0_lo_.ptr, 0, a0_lo_.bytes, stream_));
+    HIP_CHECK(hipMemsetAsync(a1_lo_.ptr, 0, a1_lo_.bytes, stream_));
+  }
+  qkv_.allocate(R * qkv_n_ * sizeof(float), "qkv");
+  q_.allocate(R * Q_ * D_ * sizeof(float), "q");
+  attn_partial_.allocate(R * Q_ * kMaxSplits * (D_ + 2) * sizeof(float), "attention partials");
+  gemm_ws_floats_ = 32ull << 20;
+  gemm_ws_.allocate(gemm_ws_floats_ * sizeof(float), "gemm workspace");
+  gemm_counter_count_ = 1 << 17;
+  gemm_counters_.allocate(gemm_counter_count_ * sizeof(int32_t), "gemm counters");
+  HIP_CHECK(hipMemsetAsync(gemm_counters_.ptr, 0, gemm_counters_.bytes, stream_));
+  if (c.final_stage) {
+    logits_.allocate(items_max_ * V_ * sizeof(float), "logits");
+    argmax_val_.allocate(items_max_ * kArgmaxParts * sizeof(float), "argmax");
+    argmax_idx_.allocate(items_max_ * kArgmaxParts * sizeof(int32_t), "argmax");
+  }
+  tokens_.allocate(items_max_ * sizeof(int32_t), "tokens");
+  flags_.allocate(sizeof(int32_t), "flags");
+  items_dev_.allocate(items_max_ * sizeof(ItemMeta), "items");
+  host_tokens_dev_.allocate(R * sizeof(int32_t), "tokens");
+  pack_buf_.allocate(((items_max_ + 1) + 4 * R + 2 * items_max_ + 1) * sizeof(int32_t), "pack");
+  {
+    int32_t* p = pack_buf_.as<int32_t>();
+    pack_.cu_seqlens = p;
+    p += items_max_ + 1;
+    pack_.row_item = p;
+    p += R;
+    pack_.row_position = p;
+    p += R;
+    pack_.row_slot = p;
+    p += R;
+    pack_.row_token = p;
+    p += R;
+    pack_.sample_row = p;
+    p += items_max_;
+    pack_.sample_item = p;
+    p += items_max_;
+    pack_.sample_count = p;
+  }
+  if (!c.first_stage || !c.final_stage) boundary_dev_.allocate(R * H_ * 2, "boundary");
+  pin_items_.allocate(items_max_ * sizeof(ItemMeta));
+  pin_tokens_.allocate(R * sizeof(int32_t));
+  pin_out_tokens_.allocate(items_max_ * sizeof(int32_t));
+  pin_flags_.allocate(sizeof(int32_t));
+  pin_boundary_.allocate(R * H_ * 2);
+  staging_.allocate(kStagingBytes, "load staging");
+
+  // ---- paged KV pool (the rest of HBM unless sized explicitly)
+  const size_t kv_el = kv_f32_ ? 4 : 2;
+  const uint64_t block_bytes_all_layers = 2 * K_ * (uint64_t)bt * D_ * kv_el * L_;
+  table_width_ = (int)((c.maximum_sequence_length + bt - 1) / bt);
+  uint64_t kv_bytes = c.kv_cache_bytes;
+  if (kv_bytes == 0) {
+    size_t free_b = 0, total_b = 0;
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    HIP_CHECK(hipMemGetInfo(&free_b, &total_b));
+    kv_bytes = (uint64_t)(0.9 * (double)free_b);
+  }
+  blocks_total_ = kv_bytes / block_bytes_all_layers;
+  if (blocks_total_ == 0) fail(HLLM_RESOURCE_EXHAUSTED, "KV cache budget holds no block");
+  if (blocks_total_ * bt > 0x7fffffffull) blocks_total_ = 0x7fffffffull / bt;
+  kv_pool_.allocate(blocks_total_ * block_bytes_all_layers, "KV cache");
+  kv_.pool = kv_pool_.ptr;
+  kv_.block_tokens = bt;
+  kv_.kv_heads = (int)K_;
+  kv_.head_dim = (int)D_;
+  kv_.f32 = kv_f32_ ? 1 : 0;
+  kv_.layer_stride = blocks_total_ * 2 * K_ * bt * D_;
+  free_blocks_.reserve(blocks_total_);
+  for (uint64_t b = blocks_total_; b-- > 0;) free_blocks_.push_back((int32_t)b);
+  sequences_.resize(seq_max);
+  for (uint64_t s = seq_max; s-- > 0;) free_slots_.push_back((uint32_t)s);
+  block_table_.allocate(seq_max * table_width_ * sizeof(int32_t), "block table");
+  HIP_CHECK(hipMemsetAsync(block_table_.ptr, 0xff, block_table_.bytes, stream_));
+  last_token_.allocate(seq_max * sizeof(int32_t), "last tokens");
+  HIP_CHECK(hipMemsetAsync(last_token_.ptr, 0, last_token_.bytes, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+Stage::~Stage() {
+  if (stream_) {
+    (void)hipStreamSynchronize(stream_);
+    for (auto& [name, p] : profiles_)
+      for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
+    for (auto e : event_pool_) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(stream_);
+  }
+}
+
+void Stage::check_sizes() {
+  const auto& c = c_;
+  if (c.hidden_size == 0 || c.intermediate_size == 0 || c.attention_heads == 0 ||
+      c.key_value_heads == 0 || c.head_dimension == 0 || c.maximum_sequence_length == 0 ||
+      c.vocabulary_size == 0 || !(c.rms_norm_epsilon > 0.0f) || !std::isfinite(c.rms_norm_epsilon) ||
+      !(c.rope_theta > 0.0f) || !std::isfinite(c.rope_theta)) {
+    fail(HLLM_INCOMPATIBLE_WORKER, "unsupported dense model configuration");
+  }
+  if (c.attention_heads % c.key_value_heads != 0 || c.layer_start >= c.layer_end)
+    fail(HLLM_INCOMPATIBLE_WORKER, "inconsistent attention heads or layer range");
+  const uint64_t d = c.head_dimension;
+  if (d < 4 || d > 256 || (d & (d - 1)) != 0)
+    fail(HLLM_INCOMPATIBLE_WORKER, "head dimension must be a power of two in [4, 256]");
+  if (c.attention_heads / c.key_value_heads > 8 || (c.attention_heads / c.key_value_heads) * d > 2048)
+    fail(HLLM_INCOMPATIBLE_WORKER, "query heads per KV head must be at most 8");
+  if (c.execution_dtype != HLLM_DTYPE_F16 && c.execution_dtype != HLLM_DTYPE_F32)
+    fail(HLLM_INCOMPATIBLE_WORKER, "execution dtype must be F16 or F32");
+  if (c.weight_dtype != HLLM_DTYPE_F16 &&
+      !(c.weight_dtype == HLLM_DTYPE_F32 && c.execution_dtype == HLLM_DTYPE_F32))
+    fail(HLLM_INCOMPATIBLE_WORKER, "unsupported resident/execution precision contract");
+  if (c.maximum_sequence_length > (1u << 24) || c.vocabulary_size > 0x7fffffffull ||
+      c.hidden_size > (1u << 16) || c.intermediate_size > (1u << 18))
+    fail(HLLM_INCOMPATIBLE_WORKER, "model dimensions exceed this worker's limits");
+  if (c.kv_block_tokens && (c.kv_block_tokens & (c.kv_block_tokens - 1)))
+    fail(HLLM_INVALID_REQUEST, "KV block tokens must be a power of two");
+  if (c.max_pass_rows > (1u << 16)) fail(HLLM_INVALID_REQUEST, "max pass rows too large");
+}
+
+// --------------------------------------------------------------------- loading
+
+Target& Stage::target(const std::string& name) {
+  if (finalized_) fail(HLLM_INVALID_REQUEST, "stage is already finalized");
+  auto it = targets_.find(name);
+  if (it == targets_.end()) fail(HLLM_INCOMPATIBLE_WORKER, "unsupported selected tensor: " + name);
+  return it->second;
+}
+
+void Stage::read_flags(const char* context) {
+  int32_t flags = 0;
+  HIP_CHECK(hipMemcpyAsync(pin_flags_.ptr, flags_.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  flags = *pin_flags_.as<int32_t>();
+  if (flags & 1) fail(HLLM_INCOMPATIBLE_WORKER, std::string("non-finite weight: ") + context);
+  if (flags & 4) fail(HLLM_INCOMPATIBLE_WORKER, std::string("weight is not representable as finite F16: ") + context);
+}
+
+void Stage::relayout(Target& t, const std::string& name, const void* device_src, uint32_t dtype,
+                     uint64_t seed, uint64_t tensor_id, float mean, float sigma, uint64_t row_base,
+                     uint64_t rows) {
+  RelayoutArgs a{};
+  a.src = device_src;
+  a.src_dtype = dtype;
+  a.seed = seed;
+  a.tensor_id = tensor_id;
+  a.mean = mean;
+  a.sigma = sigma;
+  a.rows = rows;
+  a.row_base = row_base;
+  a.cols = t.shape.size() == 2 ? t.shape[1] : t.shape[0];
+  a.f16_resident = w_f32_ ? 0 : 1;
+  a.flags = flags_.as<int32_t>();
+  if (t.matrix) {
+    a.dst_hi = t.matrix->hi.as<uint16_t>();
+    a.dst_lo = w_f32_ ? t.matrix->lo.as<uint16_t>() : nullptr;
+    a.dst_cols_padded = t.matrix->cols_padded;
+    a.row_mode = t.row_mode;
+    a.row_offset = t.row_offset;
+  } else {
+    a.dst_f32 = t.vector->as<float>();
+    a.rows = 1;
+  }
+  (void)name;
+  launch_relayout(stream_, a);
+  HIP_CHECK(hipGetLastError());
+}
+
+void Stage::load_tensor(const std::string& name, uint32_t dtype, const uint64_t* shape, uint32_t rank,
+                        const void* data, uint64_t bytes) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  Target& t = target(name);
+  if (std::vector<uint64_t>(shape, shape + rank) != t.shape)
+    fail(HLLM_INCOMPATIBLE_WORKER, "incorrect tensor shape: " + name);
+  if (dtype != HLLM_DTYPE_F32 && dtype != HLLM_DTYPE_F16 && dtype != HLLM_DTYPE_BF16)
+    fail(HLLM_INCOMPATIBLE_WORKER, "unsupported weight dtype: " + name);
+  const uint64_t el = dtype == HLLM_DTYPE_F32 ? 4 : 2;
+  const uint64_t rows = t.shape.size() == 2 ? t.shape[0] : 1;
+  const uint64_t cols = t.shape.size() == 2 ? t.shape[1] : t.shape[0];
+  if (bytes != rows * cols * el || !data) fail(HLLM_INCOMPATIBLE_WORKER, "truncated weight payload: " + name);
+  HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
+  const uint64_t row_bytes = cols * el;
+  const uint64_t chunk_rows = std::max<uint64_t>(1, kStagingBytes / row_bytes);
+  if (row_bytes > kStagingBytes) fail(HLLM_INCOMPATIBLE_WORKER, "tensor row too large: " + name);
+  for (uint64_t r0 = 0; r0 < rows; r0 += chunk_rows) {
+    const uint64_t n = std::min(chunk_rows, rows - r0);
+    HIP_CHECK(hipMemcpyAsync(staging_.ptr, static_cast<const char*>(data) + r0 * row_bytes,
+                             n * row_bytes, hipMemcpyHostToDevice, stream_));
+    relayout(t, name, staging_.ptr, dtype, 0, 0, 0.f, 0.f, r0, n);
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
+  read_flags(name.c_str());
+  t.loaded = true;
+}
+
+void Stage::synthesize(const std::string& name, uint64_t seed, uint64_t tensor_id, float mean,
+                       float sigma, uint32_t source_dtype) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  Target& t = target(name);
+  if (source_dtype != HLLM_DTYPE_F32 && source_dtype != HLLM_DTYPE_F16)
+    fail(HLLM_INVALID_REQUEST, "synthetic source dtype must be F32 or F16");
+  HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
+  const uint64_t rows = t.shape.size() == 2 ? t.shape[0] : 1;
+  relayout(t, name, nullptr, source_dtype, seed, tensor_id, mean, sigma, 0, rows);
+  read_flags(name.c_str());
+  t.loaded = true;
+}
+
+void Stage::finalize() {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  for (auto& [name, t] : targets_) {
+    if (!t.loaded) fail(HLLM_INCOMPATIBLE_WORKER, "missing required tensor: " + name);
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  staging_.release();
+  finalized_ = true;
+}
+
+// --------------------------------------------------------------------- memory accounting
+
+void Stage::sequence_memory(uint64_t tokens, uint64_t max_query, hllm_rocm_memory* cache,
+                            hllm_rocm_memory* workspace) const {
+  if (tokens == 0 || tokens > c_.maximum_sequence_length)
+    fail(HLLM_INVALID_REQUEST, "request exceeds model context capacity");
+  const uint64_t bt = kv_.block_tokens;
+  const uint64_t kv_el = kv_f32_ ? 4 : 2;
+  const uint64_t blocks = (tokens + bt - 1) / bt;
+  const uint64_t rows = (max_query == 0 || max_query > tokens) ? tokens : max_query;
+  // KV blocks come from the pool reserved at stage creation; the admission figure is the
+  // HBM they occupy. Pass workspaces are reserved up front as well, so a request adds no
+  // device workspace; the host holds its transport copies (request_transport_bytes,
+  // cpp/include/hllm/runtime/stage_backend.hpp:36-40).
+  if (cache) {
+    *cache = {tokens * 3 * 8 + rows * H_ * 6, blocks * bt * 2 * K_ * D_ * kv_el * L_, 0, 0};
+  }
+  if (workspace) *workspace = {rows * H_ * 6 + 65536, 0, 0, 0};
+}
+
+uint32_t Stage::allocate_sequence(uint64_t tokens) {
+  sequence_memory(tokens, tokens, nullptr, nullptr);
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  const uint64_t bt = kv_.block_tokens;
+  const uint64_t blocks = (tokens + bt - 1) / bt;
+  if (free_slots_.empty()) fail(HLLM_RESOURCE_EXHAUSTED, "no free sequence slot");
+  if (free_blocks_.size() < blocks) fail(HLLM_RESOURCE_EXHAUSTED, "KV cache is full");
+  const uint32_t slot = free_slots_.back();
+  Sequence& s = sequences_[slot];
+  s.blocks.assign(free_blocks_.end() - blocks, free_blocks_.end());
+  std::vector<int32_t> row(table_width_, -1);
+  std::copy(s.blocks.begin(), s.blocks.end(), row.begin());
+  HIP_CHECK(hipMemcpy(block_table_.as<int32_t>() + (size_t)slot * table_width_, row.data(),
+                      row.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+  free_blocks_.resize(free_blocks_.size() - blocks);
+  free_slots_.pop_back();
+  s.live = true;
+  s.failed = false;
+  s.capacity = tokens;
+  s.length = 0;
+  return slot;
+}
+
+void Stage::release_sequence(uint32_t handle) {
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+  Sequence& s = sequences_[handle];
+  free_blocks_.insert(free_blocks_.end(), s.blocks.begin(), s.blocks.end());
+  s = Sequence{};
+  free_slots_.push_back(handle);
+}
+
+uint64_t Stage::sequence_length(uint32_t handle) const {
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+  return sequences_[handle].length;
+}
+
+// --------------------------------------------------------------------- diagnostics
+
+void Stage::last_layout(uint32_t items, uint32_t rows, int32_t* cu, int32_t* pos, int32_t* slots) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  if (items > items_max_ || rows > rows_max_) fail(HLLM_INVALID_REQUEST, "layout request too large");
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  if (cu) HIP_CHECK(hipMemcpy(cu, pack_.cu_seqlens, (items + 1) * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (pos) HIP_CHECK(hipMemcpy(pos, pack_.row_position, rows * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (slots) HIP_CHECK(hipMemcpy(slots, pack_.row_slot, rows * sizeof(int32_t), hipMemcpyDeviceToHost));
+}
+
+void Stage::sequence_blocks(uint32_t handle, int32_t* blocks, uint32_t capacity, uint32_t* count,
+                            uint32_t* block_tokens) {
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+  const auto& b = sequences_[handle].blocks;
+  if (count) *count = (uint32_t)b.size();
+  if (block_tokens) *block_tokens = (uint32_t)kv_.block_tokens;
+  if (blocks) std::copy(b.begin(), b.begin() + std::min<size_t>(b.size(), capacity), blocks);
+}
+
+void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  std::vector<int32_t> blocks;
+  uint64_t length = 0;
+  {
+    std::lock_guard<std::mutex> sl(seq_mutex_);
+    if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+    blocks = sequences_[handle].blocks;
+    length = sequences_[handle].length;
+  }
+  if (layer >= L_) fail(HLLM_INVALID_REQUEST, "layer out of range");
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  const uint64_t bt = kv_.block_tokens, el = kv_f32_ ? 4 : 2;
+  const uint64_t head_elems = bt * D_;
+  std::vector<char> block(2 * K_ * head_elems * el);
+  for (uint64_t p0 = 0; p0 < length; p0 += bt) {
+    const uint64_t b = (uint64_t)blocks[p0 / bt];
+    const char* src = static_cast<const char*>(kv_pool_.ptr) +
+                      (layer * kv_.layer_stride + b * 2 * K_ * head_elems) * el;
+    HIP_CHECK(hipMemcpy(block.data(), src, block.size(), hipMemcpyDeviceToHost));
+    for (uint64_t p = p0; p < std::min(length, p0 + bt); ++p)
+      for (uint64_t which = 0; which < 2; ++which)
+        for (uint64_t hd = 0; hd < K_; ++hd)
+          for (uint64_t d = 0; d < D_; ++d) {
+            const uint64_t i = ((which * K_ + hd) * bt + (p - p0)) * D_ + d;
+            float v;
+            if (kv_f32_) {
+              std::memcpy(&v, block.data() + i * 4, 4);
+            } else {
+              _Float16 hv;
+              std::memcpy(&hv, block.data() + i * 2, 2);
+              v = (float)hv;
+            }
+            (which ? values : keys)[(p * K_ + hd) * D_ + d] = v;
+          }
+  }
+}
+
+// --------------------------------------------------------------------- profiling
+
+template <typename F>
+void Stage::timed(const char* family, uint64_t bytes, F&& launch) {
+  if (!profiling_) {
+    launch();
+    return;
+  }
+  auto take = [&] {
+    if (event_pool_.empty()) {
+      hipEvent_t e;
+      HIP_CHECK(hipEventCreate(&e));
+      return e;
+    }
+    hipEvent_t e = event_pool_.back();
+    event_pool_.pop_back();
+    return e;
+  };
+  hipEvent_t start = take(), stop = take();
+  HIP_CHECK(hipEventRecord(start, stream_));
+  launch();
+  HIP_CHECK(hipEventRecord(stop, stream_));
+  Profile& p = profiles_[family];
+  p.events.emplace_back(start, stop);
+  p.bytes += bytes;
+}
+
+void Stage::set_profiling(bool on) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  for (auto& [name, p] : profiles_)
+    for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
+  profiles_.clear();
+  profiling_ = on;
+}
+
+void Stage::profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  double total = 0.0;
+  uint64_t n = 0, b = 0;
+  for (auto& [name, p] : profiles_) {
+    if (!(name == family || (family.back() == '*' && name.compare(0, family.size() - 1, family, 0,
+                                                                  family.size() - 1) == 0)))
+      continue;
+    for (auto& e : p.events) {
+      float t = 0.f;
+      HIP_CHECK(hipEventElapsedTime(&t, e.first, e.second));
+      total += t;
+    }
+    n += p.events.size();
+    b += p.bytes;
+  }
+  *ms = total;
+  *launches = n;
+  *bytes = b;
+}
+
+// --------------------------------------------------------------------- the pass
+
+void Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo,
+                 int rows, int n, int epilogue, float* out, int ldo, uint16_t* out_hi,
+                 uint16_t* out_lo, uint64_t out_cols_padded) {
+  GemmArgs a{};
+  a.w_hi = w.hi.as<uint16_t>();
+  a.w_lo = w.lo.as<uint16_t>();
+  a.x_hi = x_hi;
+  a.x_lo = x_lo;
+  a.M = rows;
+  a.N = n;
+  a.Kp = w.cols_padded;
+  a.workspace = gemm_ws_.as<float>();
+  a.workspace_floats = gemm_ws_floats_;
+  a.counters = gemm_counters_.as<int32_t>();
+  a.counter_count = gemm_counter_count_;
+  a.epilogue = epilogue;
+  a.out = out;
+  a.ldo = ldo;
+  a.out_hi = out_hi;
+  a.out_lo = out_lo;
+  a.out_cols_padded = out_cols_padded;
+  const uint64_t wbytes = (uint64_t)n * w.cols_padded * 2 * (w_f32_ ? 2 : 1);
+  const uint64_t xbytes = (uint64_t)rows * w.cols_padded * 2 * (x_lo ? 2 : 1);
+  const uint64_t obytes = epilogue == kEpiSwiglu ? (uint64_t)rows * (n / 2) * 2 * (out_lo ? 2 : 1)
+                                                 : (uint64_t)rows * n * 4 * (epilogue == kEpiResidual ? 2 : 1);
+  timed(family, wbytes + xbytes + obytes, [&] { launch_gemm(stream_, a, prec_, rows, cus_); });
+}
+
+void Stage::fail_pass(const std::vector<uint32_t>& sequences) {
+  (void)hipStreamSynchronize(stream_);
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  for (uint32_t s : sequences)
+    if (s < sequences_.size()) sequences_[s].failed = true;
+}
+
+void Stage::submit(const hllm_rocm_pass& pass) {
+  std::unique_lock<std::mutex> lock(pass_mutex_);
+  if (!finalized_) fail(HLLM_INVALID_REQUEST, "stage is not finalized");
+  if (in_flight_) fail(HLLM_INVALID_REQUEST, "a pass is already in flight");
+  const uint32_t n = pass.items;
+  if (n == 0 || n > items_max_ || !pass.item) fail(HLLM_INVALID_REQUEST, "invalid pass size");
+  // ---- validate on the host (positions, capacities, inputs) before touching the device
+  uint64_t rows = 0;
+  std::vector<uint32_t> seqs(n);
+  std::vector<int> sample_items;
+  {
+    std::lock_guard<std::mutex> sl(seq_mutex_);
+    std::set<uint32_t> unique;
+    for (uint32_t i = 0; i < n; ++i) {
+      const hllm_rocm_item& it = pass.item[i];
+      if (it.sequence >= sequences_.size() || !sequences_[it.sequence].live)
+        fail(HLLM_INVALID_REQUEST, "unknown sequence");
+      const Sequence& s = sequences_[it.sequence];
+      if (s.failed || it.first_position != s.length || it.query_tokens == 0 ||
+          it.query_tokens > s.capacity - std::min(s.capacity, s.length) ||
+          !unique.insert(it.sequence).second)
+        fail(HLLM_INVALID_REQUEST, "invalid sequence state, position or context capacity");
+      if ((it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) && (!c_.first_stage || it.query_tokens != 1 || s.length == 0))
+        fail(HLLM_INVALID_REQUEST, "device-fed input needs one token of a started sequence");
+      if (it.flags & HLLM_ITEM_SAMPLE) {
+        if (!(it.temperature >= 0.0 && it.temperature <= 100.0) || !(it.top_p > 0.0 && it.top_p <= 1.0) ||
+            it.top_logprobs > 5 || (!(it.flags & HLLM_ITEM_LOGPROBS) && it.top_logprobs != 0))
+          fail(HLLM_INVALID_REQUEST, "invalid sampling parameters");
+        if (it.temperature != 0.0 || (it.flags & HLLM_ITEM_LOGPROBS))
+          fail(HLLM_INCOMPATIBLE_WORKER, "device sampling supports greedy decoding only");
+        if (c_.final_stage) sample_items.push_back((int)i);
+      }
+      seqs[i] = it.sequence;
+      rows += it.query_tokens;
+    }
+  }
+  if (rows > rows_max_) fail(HLLM_RESOURCE_EXHAUSTED, "pass exceeds the stage's row budget");
+  if (c_.first_stage && !pass.token_ids) fail(HLLM_INVALID_REQUEST, "stage zero requires tokens");
+  if (!c_.first_stage && !pass.boundary_in) fail(HLLM_INVALID_REQUEST, "only stage zero accepts tokens");
+  ItemMeta* meta = pin_items_.as<ItemMeta>();
+  int32_t* host_tokens = pin_tokens_.as<int32_t>();
+  {
+    uint64_t r = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+      const hllm_rocm_item& it = pass.item[i];
+      meta[i] = {it.sequence, it.query_tokens, (uint32_t)it.first_position, it.flags};
+      for (uint32_t j = 0; j < it.query_tokens; ++j, ++r) {
+        if (c_.first_stage) {
+          const bool from_device = it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE;
+          const uint64_t id = from_device ? 0 : pass.token_ids[r];
+          if (id >= V_) fail(HLLM_INVALID_REQUEST, "token ID exceeds vocabulary");
+          host_tokens[r] = (int32_t)id;
+        }
+      }
+    }
+  }
+  if (!c_.first_stage) {
+    const uint64_t count = rows * H_;
+    for (uint64_t i = 0; i < count; ++i) {
+      if ((pass.boundary_in[i] & 0x7c00u) == 0x7c00u) fail(HLLM_INVALID_REQUEST, "non-finite activation");
+    }
+    std::memcpy(pin_boundary_.ptr, pass.boundary_in, count * 2);
+  }
+  if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+
+  // ---- device work
+  try {
+    const int R = (int)rows;
+    const int S = (int)sample_items.size();
+    HIP_CHECK(hipMemcpyAsync(items_dev_.ptr, meta, n * sizeof(ItemMeta), hipMemcpyHostToDevice, stream_));
+    HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
+    if (c_.first_stage)
+      HIP_CHECK(hipMemcpyAsync(host_tokens_dev_.ptr, host_tokens, R * sizeof(int32_t), hipMemcpyHostToDevice,
+                               stream_));
+    timed("pack", 0, [&] {
+      launch_pack(stream_, items_dev_.as<ItemMeta>(), (int)n, host_tokens_dev_.as<int32_t>(),
+                  last_token_.as<int32_t>(), block_table_.as<int32_t>(), table_width_, kv_.block_tokens, pack_);
+    });
+    float* h = h_.as<float>();
+    if (c_.first_stage) {
+      timed("embed", (uint64_t)R * H_ * 6, [&] {
+        launch_embed(stream_, embedding_.hi.as<uint16_t>(), w_f32_ ? embedding_.lo.as<uint16_t>() : nullptr,
+                     embedding_.cols_padded, pack_.row_token, R, (int)H_, h);
+      });
+    } else {
+      HIP_CHECK(hipMemcpyAsync(boundary_dev_.ptr, pin_boundary_.ptr, (size_t)R * H_ * 2, hipMemcpyHostToDevice,
+                               stream_));
+      timed("boundary", (uint64_t)R * H_ * 6,
+            [&] { launch_boundary_decode(stream_, boundary_dev_.as<uint16_t>(), R, (int)H_, h); });
+    }
+    uint16_t* a0h = a0_hi_.as<uint16_t>();
+    uint16_t* a0l = a0_lo_.as<uint16_t>();
+    uint16_t* a1h = a1_hi_.as<uint16_t>();
+    uint16_t* a1l = a1_lo_.as<uint16_t>();
+    const float eps = c_.rms_norm_epsilon;
+    const uint64_t a1_cols = std::max(QDp_, Ip_);
+    (void)a1_cols;
+    for (uint64_t l = 0; l < L_; ++l) {
+      if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+      Layer& w = *layers_[l];
+      timed("norm", (uint64_t)R * H_ * 6, [&] {
+        launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.input_norm.as<float>(), eps, a0h, a0l,
+                               Hp_);
+      });
+      gemm("gemm_qkv", w.qkv, a0h, a0l, R, (int)qkv_n_, kEpiStore, qkv_.as<float>(), (int)qkv_n_, nullptr,
+           nullptr, 0);
+      timed("rope_append", (uint64_t)R * qkv_n_ * 6, [&] {
+        launch_qkv_rope_append(stream_, qkv_.as<float>(), R, (int)Q_, (int)K_, (int)D_,
+                               c_.query_key_norm ? w.q_norm.as<float>() : nullptr,
+                               c_.query_key_norm ? w.k_norm.as<float>() : nullptr, eps, rope_cos_.as<float>(),
+                               rope_sin_.as<float>(), pack_.row_position, pack_.row_slot, kv_, (int)l,
+                               q_.as<float>());
+      });
+      AttentionArgs at{};
+      at.q = q_.as<float>();
+      at.rows = R;
+      at.q_heads = (int)Q_;
+      at.kv_heads = (int)K_;
+      at.head_dim = (int)D_;
+      at.row_item = pack_.row_item;
+      at.row_position = pack_.row_position;
+      at.items = items_dev_.as<ItemMeta>();
+      at.block_table = block_table_.as<int32_t>();
+      at.table_width = table_width_;
+      at.kv = kv_;
+      at.layer = (int)l;
+      at.scale = 1.0f / std::sqrt(static_cast<float>(D_));
+      at.partial = attn_partial_.as<float>();
+      at.max_splits = kMaxSplits;
+      at.split_unit = kSplitUnit;
+      at.out_hi = a1h;
+      at.out_lo = a1l;
+      at.out_cols_padded = QDp_;
+      timed("attention", 0, [&] { launch_attention(stream_, at); });
+      gemm("gemm_o", w.o, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0);
+      timed("norm", (uint64_t)R * H_ * 6, [&] {
+        launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.post_norm.as<float>(), eps, a0h, a0l,
+                               Hp_);
+      });
+      gemm("gemm_gate_up", w.gate_up, a0h, a0l, R, (int)(2 * Ip_), kEpiSwiglu, nullptr, 0, a1h, a1l, Ip_);
+      gemm("gemm_down", w.down, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0);
+      HIP_CHECK(hipGetLastError());
+      if (pass.trace_hidden) {
+        HIP_CHECK(hipMemcpyAsync(pass.trace_hidden + l * (size_t)R * H_, h, (size_t)R * H_ * sizeof(float),
+                                 hipMemcpyDeviceToHost, stream_));
+        HIP_CHECK(hipStreamSynchronize(stream_));
+      }
+    }
+    if (c_.final_stage) {
+      if (S > 0) {
+        timed("norm", (uint64_t)S * H_ * 6, [&] {
+          launch_rmsnorm_flayout(stream_, h, (int)H_, pack_.sample_row, S, nullptr, final_norm_.as<float>(), eps,
+                                 a0h, a0l, Hp_);
+        });
+        const Matrix& head = c_.tied_head ? embedding_ : head_;
+        gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
+             nullptr, 0);
+        timed("argmax", (uint64_t)S * V_ * 4, [&] {
+          launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
+                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_.as<int32_t>());
+        });
+        launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
+                             items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
+        HIP_CHECK(hipMemcpyAsync(pin_out_tokens_.ptr, tokens_.ptr, S * sizeof(int32_t), hipMemcpyDeviceToHost,
+                                 stream_));
+        if (pass.logits)
+          HIP_CHECK(hipMemcpyAsync(pass.logits, logits_.ptr, (size_t)S * V_ * sizeof(float),
+                                   hipMemcpyDeviceToHost, stream_));
+      }
+    } else {
+      timed("boundary", (uint64_t)R * H_ * 6, [&] {
+        launch_boundary_encode(stream_, h, R, (int)H_, boundary_dev_.as<uint16_t>(), flags_.as<int32_t>());
+      });
+      HIP_CHECK(hipMemcpyAsync(pin_boundary_.ptr, boundary_dev_.ptr, (size_t)R * H_ * 2, hipMemcpyDeviceToHost,
+                               stream_));
+    }
+    HIP_CHECK(hipMemcpyAsync(pin_flags_.ptr, flags_.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+    HIP_CHECK(hipGetLastError());
+  } catch (...) {
+    fail_pass(seqs);
+    throw;
+  }
+  in_flight_ = true;
+  pending_ = pass;
+  pending_sequences_ = seqs;
+  pending_lengths_.assign(n, 0);
+  for (uint32_t i = 0; i < n; ++i) pending_lengths_[i] = pass.item[i].query_tokens;
+  pending_sample_items_ = sample_items;
+  pending_rows_ = rows;
+}
+
+void Stage::wait() {
+  std::unique_lock<std::mutex> lock(pass_mutex_);
+  if (!in_flight_) fail(HLLM_INVALID_REQUEST, "no pass in flight");
+  in_flight_ = false;
+  const hipError_t e = hipStreamSynchronize(stream_);
+  if (e != hipSuccess) {
+    fail_pass(pending_sequences_);
+    check_hip(e, "pass");
+  }
+  const int32_t flags = *pin_flags_.as<int32_t>();
+  if (flags & 2) {
+    fail_pass(pending_sequences_);
+    fail(HLLM_INTERNAL, "cannot sample nonfinite logits");
+  }
+  if (flags & 4) {
+    fail_pass(pending_sequences_);
+    fail(HLLM_INTERNAL, "activation is not representable as finite FP16");
+  }
+  const hllm_rocm_pass& pass = pending_;
+  if (c_.final_stage && pass.tokens) {
+    for (uint32_t i = 0; i < pass.items; ++i) pass.tokens[i] = UINT64_MAX;
+    const int32_t* t = pin_out_tokens_.as<int32_t>();
+    for (size_t j = 0; j < pending_sample_items_.size(); ++j) pass.tokens[pending_sample_items_[j]] = (uint64_t)t[j];
+  }
+  if (!c_.final_stage && pass.boundary_out) std::memcpy(pass.boundary_out, pin_boundary_.ptr, pending_rows_ * H_ * 2);
+  std::lock_guard<std::mutex> sl(seq_mutex_);
+  for (size_t i = 0; i < pending_sequences_.size(); ++i) sequences_[pending_sequences_[i]].length += pending_lengths_[i];
+}
+
+}  // namespace hllm_rocm
+
+// ========================================================================= C ABI
+
+using hllm_rocm::Failure;
+using hllm_rocm::Stage;
+
+struct hllm_rocm_stage {
+  std::unique_ptr<Stage> impl;
+};
+
+namespace {
+template <typename F>
+hllm_status guarded(F&& f) {
+  try {
+    f();
+    return HLLM_OK;
+  } catch (const Failure& e) {
+    hllm_rocm::g_last_error = e.what();
+    return e.status;
+  } catch (const std::bad_alloc&) {
+    hllm_rocm::g_last_error = "host allocation failed";
+    return HLLM_RESOURCE_EXHAUSTED;
+  } catch (const std::exception& e) {
+    hllm_rocm::g_last_error = e.what();
+    return HLLM_INTERNAL;
+  } catch (...) {
+    hllm_rocm::g_last_error = "unknown failure";
+    return HLLM_INTERNAL;
+  }
+}
+Stage& impl(hllm_rocm_stage* s) {
+  if (!s || !s->impl) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null stage");
+  return *s->impl;
+}
+const Stage& impl(const hllm_rocm_stage* s) {
+  if (!s || !s->impl) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null stage");
+  return *s->impl;
+}
+}  // namespace
+
+extern "C" {
+
+const char* hllm_rocm_last_error(void) { return hllm_rocm::g_last_error.c_str(); }
+uint32_t hllm_rocm_abi_version(void) { return HLLM_ROCM_ABI_VERSION; }
+
+hllm_status hllm_rocm_stage_create(const hllm_rocm_stage_config* config, hllm_rocm_stage** out) {
+  return guarded([&] {
+    if (!config || !out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    *out = nullptr;
+    auto s = std::make_unique<hllm_rocm_stage>();
+    s->impl = std::make_unique<Stage>(*config);
+    *out = s.release();
+  });
+}
+
+void hllm_rocm_stage_destroy(hllm_rocm_stage* stage) { delete stage; }
+
+hllm_status hllm_rocm_stage_load_tensor(hllm_rocm_stage* stage, const char* name, uint32_t dtype,
+                                        const uint64_t* shape, uint32_t rank, const void* data, uint64_t bytes) {
+  return guarded([&] {
+    if (!name || (!shape && rank)) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).load_tensor(name, dtype, shape, rank, data, bytes);
+  });
+}
+
+hllm_status hllm_rocm_stage_synthesize_tensor(hllm_rocm_stage* stage, const char* name, uint64_t seed,
+                                              uint64_t tensor_id, float mean, float sigma, uint32_t source_dtype) {
+  return guarded([&] {
+    if (!name) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).synthesize(name, seed, tensor_id, mean, sigma, source_dtype);
+  });
+}
+
+hllm_status hllm_rocm_stage_finalize(hllm_rocm_stage* stage) {
+  return guarded([&] { impl(stage).finalize(); });
+}
+
+hllm_status hllm_rocm_stage_weight_memory(const hllm_rocm_stage* stage, hllm_rocm_memory* out) {
+  return guarded([&] {
+    if (!out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    *out = impl(stage).weight_memory();
+  });
+}
+
+hllm_status hllm_rocm_stage_sequence_memory(const hllm_rocm_stage* stage, uint64_t tokens,
+                                            uint64_t maximum_query_tokens, hllm_rocm_memory* cache,
+                                            hllm_rocm_memory* workspace) {
+  return guarded([&] { impl(stage).sequence_memory(tokens, maximum_query_tokens, cache, workspace); });
+}
+
+hllm_status hllm_rocm_sequence_allocate(hllm_rocm_stage* stage, uint64_t tokens, uint32_t* sequence) {
+  return guarded([&] {
+    if (!sequence) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    *sequence = impl(stage).allocate_sequence(tokens);
+  });
+}
+
+hllm_status hllm_rocm_sequence_release(hllm_rocm_stage* stage, uint32_t sequence) {
+  return guarded([&] { impl(stage).release_sequence(sequence); });
+}
+
+hllm_status hllm_rocm_sequence_length(const hllm_rocm_stage* stage, uint32_t sequence, uint64_t* length) {
+  return guarded([&] {
+    if (!length) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    *length = impl(stage).sequence_length(sequence);
+  });
+}
+
+hllm_status hllm_rocm_stage_submit(hllm_rocm_stage* stage, const hllm_rocm_pass* pass) {
+  return guarded([&] {
+    if (!pass) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).submit(*pass);
+  });
+}
+
+hllm_status hllm_rocm_stage_wait(hllm_rocm_stage* stage) {
+  return guarded([&] { impl(stage).wait(); });
+}
+
+hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass* pass) {
+  const hllm_status s = hllm_rocm_stage_submit(stage, pass);
+  if (s != HLLM_OK) return s;
+  return hllm_rocm_stage_wait(stage);
+}
+
+hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, uint32_t rows,
+                                        int32_t* cu_seqlens, int32_t* row_positions, int32_t* row_slots) {
+  return guarded([&] { impl(stage).last_layout(items, rows, cu_seqlens, row_positions, row_slots); });
+}
+
+hllm_status hllm_rocm_sequence_blocks(hllm_rocm_stage* stage, uint32_t sequence, int32_t* blocks,
+                                      uint32_t capacity, uint32_t* count, uint32_t* block_tokens) {
+  return guarded([&] { impl(stage).sequence_blocks(sequence, blocks, capacity, count, block_tokens); });
+}
+
+hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer, float* keys,
+                                       float* values) {
+  return guarded([&] {
+    if (!keys || !values) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).read_kv(sequence, layer, keys, values);
+  });
+}
+
+hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, int32_t enable) {
+  return guarded([&] { impl(stage).set_profiling(enable != 0); });
+}
+
+hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family, double* milliseconds,
+                                         uint64_t* launches, uint64_t* bytes) {
+  return guarded([&] {
+    if (!family || !milliseconds || !launches || !bytes) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).profile_read(family, milliseconds, launches, bytes);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,190 @@
+/*
+ * hllm_rocm: MI355X (gfx950) decoder stage worker, C ABI.
+ *
+ * One `hllm_rocm_stage` is one loaded stage (a contiguous layer range, plus the token
+ * embedding on the first stage and final norm + LM head + sampling on the last) on one
+ * GPU. It is the device side of an hLLM `runtime::StageBackend`
+ * (cpp/include/hllm/runtime/stage_backend.hpp:69-107) created by a `BackendFactory`
+ * (cpp/include/hllm/runtime/backend_factory.hpp:28-47). Plain pointers and sizes only;
+ * no exceptions cross this boundary. Every call returns an `hllm_status`; on failure,
+ * `hllm_rocm_last_error()` holds a message for the calling thread.
+ *
+ * Threading mirrors the reference contract: passes on one stage are serialized by the
+ * caller's scheduler (cpp/src/worker/scheduler.cpp:60-112); sequence allocation and
+ * release may run concurrently with a pass and take the stage's own lock
+ * (cpp/src/cuda/stage.cpp:185-202,345).
+ */
+#ifndef HLLM_ROCM_H
+#define HLLM_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HLLM_ROCM_ABI_VERSION 1u
+
+/* runtime::ErrorCode (cpp/include/hllm/runtime/error.hpp:10-17), numbered from 1. */
+typedef enum {
+  HLLM_OK = 0,
+  HLLM_INVALID_REQUEST = 1,
+  HLLM_INCOMPATIBLE_WORKER = 2,
+  HLLM_RESOURCE_EXHAUSTED = 3,
+  HLLM_DEADLINE_EXCEEDED = 4,
+  HLLM_CANCELLED = 5,
+  HLLM_INTERNAL = 6,
+} hllm_status;
+
+/* runtime::DataType subset used by dense checkpoints (cpp/include/hllm/runtime/safetensors.hpp:15-29). */
+typedef enum { HLLM_DTYPE_F32 = 0, HLLM_DTYPE_F16 = 1, HLLM_DTYPE_BF16 = 2 } hllm_dtype;
+
+typedef struct hllm_rocm_stage hllm_rocm_stage;
+
+/* model::DenseConfig + model::DenseSource ownership (cpp/include/hllm/model/dense_source.hpp:15-44)
+ * + the device resources of this worker. */
+typedef struct {
+  uint32_t abi_version;             /* HLLM_ROCM_ABI_VERSION */
+  uint64_t hidden_size;
+  uint64_t intermediate_size;
+  uint64_t attention_heads;
+  uint64_t key_value_heads;
+  uint64_t head_dimension;
+  uint64_t maximum_sequence_length;
+  uint64_t vocabulary_size;
+  float rms_norm_epsilon;
+  float rope_theta;
+  uint32_t query_key_norm;          /* Qwen3 per-head q/k RMSNorm */
+  uint32_t layer_start, layer_end;  /* owned layers [start, end) */
+  uint32_t first_stage;             /* owns the token embedding */
+  uint32_t final_stage;             /* owns final norm, LM head, sampling */
+  uint32_t tied_head;               /* LM head is the token embedding */
+  uint32_t execution_dtype;         /* HLLM_DTYPE_F16 or HLLM_DTYPE_F32 (plan execution dtype) */
+  uint32_t weight_dtype;            /* resident weights: F16, or F32 with F32 execution */
+  int32_t device;                   /* HIP device ordinal */
+  uint64_t kv_cache_bytes;          /* paged KV pool size; 0 = 90% of free HBM after weights */
+  uint32_t kv_block_tokens;         /* tokens per KV block (power of two); 0 = 64 */
+  uint32_t max_sequences;           /* live sequence slots; 0 = 512 */
+  uint32_t max_pass_rows;           /* rows per pass (prefill chunks + decode rows); 0 = 2048 */
+} hllm_rocm_stage_config;
+
+/* One request's share of a pass. */
+typedef struct {
+  uint32_t sequence;        /* handle from hllm_rocm_sequence_allocate */
+  uint32_t query_tokens;    /* rows this item contributes (prefill chunk length, or 1) */
+  uint64_t first_position;  /* must equal the sequence's current length */
+  uint32_t flags;           /* HLLM_ITEM_* */
+  uint32_t top_logprobs;    /* 0..5, with return_logprobs */
+  double temperature;       /* runtime::SamplingOptions (cpp/include/hllm/runtime/sampling.hpp:10-17) */
+  double top_p;
+  uint64_t top_k;
+  uint64_t seed;
+  uint64_t generated_index; /* counter of the sequence's sampling RNG */
+} hllm_rocm_item;
+
+/* The final stage projects the item's last row and samples a token (otherwise the item
+ * only extends the KV cache: PrefillProgress, cpp/src/cpu/stage.cpp:164). */
+#define HLLM_ITEM_SAMPLE 1u
+/* The item's single input token is the token its sequence sampled in its previous pass,
+ * read on the device (no host round trip). First stage only. */
+#define HLLM_ITEM_TOKEN_FROM_DEVICE 2u
+/* Return log-probabilities (runtime::SampledToken, cpp/src/sampling.cpp:65-89). */
+#define HLLM_ITEM_LOGPROBS 4u
+
+/* A ragged pass: any mix of prefill chunks and decode rows, rows packed in item order. */
+typedef struct {
+  uint32_t items;
+  const hllm_rocm_item* item;
+  const uint64_t* token_ids;     /* first stage: sum(query_tokens) IDs in item order */
+  const uint16_t* boundary_in;   /* other stages: [sum(query_tokens), hidden] F16 LE */
+  const volatile int32_t* cancelled; /* optional; polled between layers */
+  /* outputs (host pointers; NULL = not wanted) */
+  uint64_t* tokens;              /* final stage: [items]; items without SAMPLE get UINT64_MAX */
+  double* logprobs;              /* [items] with HLLM_ITEM_LOGPROBS */
+  uint64_t* top_ids;             /* [items * 5] */
+  double* top_logprobs;          /* [items * 5] */
+  uint16_t* boundary_out;        /* non-final: [sum(query_tokens), hidden] F16 LE */
+  float* logits;                 /* final: [sampled items, vocabulary] F32, for tests */
+  float* trace_hidden;           /* [owned layers, sum(query_tokens), hidden] F32, for tests */
+} hllm_rocm_pass;
+
+typedef struct {
+  uint64_t host_bytes;
+  uint64_t device_bytes;
+  uint64_t pinned_host_bytes;
+  uint64_t unified_bytes;
+} hllm_rocm_memory;  /* runtime::MemoryAmounts (cpp/include/hllm/runtime/memory.hpp:11-17) */
+
+/* Thread-local message of the last failed call on this thread. */
+const char* hllm_rocm_last_error(void);
+uint32_t hllm_rocm_abi_version(void);
+
+/* Stage construction, replacing the CUDA worker's CudaStage constructor
+ * (cpp/src/cuda/stage.cpp:87-144) and the CPU loader (cpp/src/cpu/stage.cpp:207-255):
+ * validate the configuration and reserve every device buffer up front. */
+hllm_status hllm_rocm_stage_create(const hllm_rocm_stage_config* config, hllm_rocm_stage** out);
+void hllm_rocm_stage_destroy(hllm_rocm_stage* stage);
+
+/* Upload one checkpoint tensor (Safetensors name and row-major LE payload), replacing the
+ * per-tensor read + upload of cpp/src/cuda/stage.cpp:123-143. Rejects unknown names,
+ * wrong shapes, non-finite values (cpp/src/model/dense_source.cpp:151-153) and values
+ * not representable as finite F16 for F16 residency (cpp/src/cuda/stage.cpp:126-133). */
+hllm_status hllm_rocm_stage_load_tensor(hllm_rocm_stage* stage, const char* name, uint32_t dtype,
+                                        const uint64_t* shape, uint32_t rank, const void* data,
+                                        uint64_t bytes);
+/* Fill one tensor with the seeded synthetic values (hllm_amd/synthetic.py) on the device. */
+hllm_status hllm_rocm_stage_synthesize_tensor(hllm_rocm_stage* stage, const char* name,
+                                              uint64_t seed, uint64_t tensor_id, float mean,
+                                              float sigma, uint32_t source_dtype);
+/* Verify that every owned tensor arrived; the stage accepts passes afterwards. */
+hllm_status hllm_rocm_stage_finalize(hllm_rocm_stage* stage);
+
+/* StageBackend::weight_memory / sequence_memory (stage_backend.hpp:72-83). */
+hllm_status hllm_rocm_stage_weight_memory(const hllm_rocm_stage* stage, hllm_rocm_memory* out);
+hllm_status hllm_rocm_stage_sequence_memory(const hllm_rocm_stage* stage, uint64_t tokens,
+                                            uint64_t maximum_query_tokens,
+                                            hllm_rocm_memory* cache, hllm_rocm_memory* workspace);
+
+/* StageBackend::allocate_sequence (stage_backend.hpp:84-85): reserve paged KV for `tokens`
+ * positions; release returns the blocks (SequenceState destruction). */
+hllm_status hllm_rocm_sequence_allocate(hllm_rocm_stage* stage, uint64_t tokens, uint32_t* sequence);
+hllm_status hllm_rocm_sequence_release(hllm_rocm_stage* stage, uint32_t sequence);
+hllm_status hllm_rocm_sequence_length(const hllm_rocm_stage* stage, uint32_t sequence,
+                                      uint64_t* length);
+
+/* StageBackend::execute / execute_decode_batch (stage_backend.hpp:90-101), generalised to
+ * ragged passes that mix prefill chunks with decode rows. Synchronous: outputs are on the
+ * host when it returns. A pass that fails after touching the KV cache poisons its
+ * sequences (cpp/src/cuda/stage.cpp:463-468). */
+hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass* pass);
+
+/* The same pass, enqueued on the stage's stream without waiting; outputs are valid after
+ * hllm_rocm_stage_wait. At most one pass is in flight per stage. */
+hllm_status hllm_rocm_stage_submit(hllm_rocm_stage* stage, const hllm_rocm_pass* pass);
+hllm_status hllm_rocm_stage_wait(hllm_rocm_stage* stage);
+
+/* Diagnostics for parity tests, like the reference's traced execution
+ * (cpp/include/hllm/cuda/stage.hpp:8-21): the last pass's device-built packing
+ * (cu_seqlens [items + 1], per-row positions and KV slots [rows]), a sequence's physical
+ * KV blocks (in logical order), and one layer's cached K and V as F32 [length, kv_heads,
+ * head_dim] (the CPU cache order, cpp/src/cpu/llama.cpp:152-158). */
+hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, uint32_t rows,
+                                        int32_t* cu_seqlens, int32_t* row_positions,
+                                        int32_t* row_slots);
+hllm_status hllm_rocm_sequence_blocks(hllm_rocm_stage* stage, uint32_t sequence, int32_t* blocks,
+                                      uint32_t capacity, uint32_t* count, uint32_t* block_tokens);
+hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer,
+                                       float* keys, float* values);
+
+/* Profiling hooks for benchmarks: HIP events around every launch of one kernel family
+ * ("gemm_decode", "attention", ...), summed per family since the last reset. */
+hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, int32_t enable);
+hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family,
+                                         double* milliseconds, uint64_t* launches,
+                                         uint64_t* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

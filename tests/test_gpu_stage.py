@@ -1,0 +1,333 @@
+"""GPU parity of the stage worker against the oracle and the reference's golden vectors,
+through the C ABI.
+
+Tolerances: F32 execution 3e-5 and F16 execution 5e-3 on the tiny Transformers fixture
+(the reference's own CUDA-backend bars, hLLM tests/cpp/cuda_stage_test.cpp:102); synthetic
+Qwen3-shaped slices in F16 execution: max-abs <= 2e-2 and cosine >= 0.9999 against the F32
+CPU oracle; F32 execution (split-precision GEMMs, F32 KV): 1e-4.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from hllm_amd import capi, model, synthetic
+from tests import models
+
+pytestmark = pytest.mark.gpu
+KV_BYTES = 256 << 20
+
+
+def _say(*what):
+    print("[gpu-case]", *what, flush=True)
+
+
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def tiny_stage(execution, layer_start=0, layer_end=2, first=True, final=True):
+    shape = models.tiny_reference_shape()
+    cfg = model.stage_config(shape, layer_start, layer_end, first, final, execution=execution,
+                             weights="f32" if execution == "f32" else "f16",
+                             kv_cache_bytes=4 << 20, max_sequences=8, max_pass_rows=64)
+    st = capi.Stage(cfg)
+    w = models.tiny_reference_stage(layer_start, layer_end, first, final)
+    model.load(st, w.tensors)
+    return st
+
+
+@pytest.mark.parametrize("execution,tol", [("f32", 3e-5), ("f16", 5e-3)])
+def test_tiny_reference_prefill_layers_kv_logits(execution, tol):
+    _say("tiny-reference prefill", execution)
+    fx = models.tiny_reference()
+    st = tiny_stage(execution)
+    seq = st.allocate(32)
+    out = st.execute([capi.item(seq, 5, 0)], token_ids=[1, 4, 2, 8, 3], want_logits=True,
+                     trace=True)
+    for layer in range(2):
+        np.testing.assert_allclose(out["trace"][layer],
+                                   models.tiny_rows(fx["layer_outputs"][layer], 0, 5), atol=tol,
+                                   rtol=0)
+        k, v = st.read_kv(seq, layer)
+        ek = np.asarray(fx["keys"][layer]["values"], np.float32).reshape(2, 5, 4).transpose(1, 0, 2)
+        ev = np.asarray(fx["values"][layer]["values"], np.float32).reshape(2, 5, 4).transpose(
+            1, 0, 2)
+        np.testing.assert_allclose(k, ek, atol=tol, rtol=0)
+        np.testing.assert_allclose(v, ev, atol=tol, rtol=0)
+    np.testing.assert_allclose(out["logits"][0], models.tiny_rows(fx["logits"], 4, 1)[0],
+                               atol=tol, rtol=0)
+    assert out["tokens"][0] == int(np.argmax(models.tiny_rows(fx["logits"], 4, 1)))
+    assert st.length(seq) == 5
+    st.close()
+
+
+def test_tiny_reference_prefill_then_two_decodes():
+    _say("tiny-reference prefill + decodes")
+    fx = models.tiny_reference()
+    st = tiny_stage("f32")
+    seq = st.allocate(32)
+    ids = [1, 4, 2, 8, 3]
+    for position, count in ((0, 3), (3, 1), (4, 1)):
+        out = st.execute([capi.item(seq, count, position)], token_ids=ids[position:position + count],
+                         want_logits=True, trace=True)
+        for layer in range(2):
+            np.testing.assert_allclose(out["trace"][layer],
+                                       models.tiny_rows(fx["layer_outputs"][layer], position, count),
+                                       atol=3e-5, rtol=0)
+        np.testing.assert_allclose(out["logits"][0],
+                                   models.tiny_rows(fx["logits"], position + count - 1, 1)[0],
+                                   atol=3e-5, rtol=0)
+    st.close()
+
+
+def test_tiny_reference_split_stages_over_f16_boundary():
+    _say("tiny-reference split stages")
+    fx = models.tiny_reference()
+    first = tiny_stage("f32", 0, 1, True, False)
+    last = tiny_stage("f32", 1, 2, False, True)
+    s0, s1 = first.allocate(32), last.allocate(32)
+    out0 = first.execute([capi.item(s0, 5, 0)], token_ids=[1, 4, 2, 8, 3])
+    expect_wire = oracle.f16_encode(models.tiny_rows(fx["layer_outputs"][0], 0, 5))
+    assert np.abs(oracle.f16_decode(out0["boundary"]) - oracle.f16_decode(expect_wire)).max() < 1e-3
+    out1 = last.execute([capi.item(s1, 5, 0)], boundary=out0["boundary"], trace=True)
+    np.testing.assert_allclose(out1["trace"][0], models.tiny_rows(fx["layer_outputs"][1], 0, 5),
+                               atol=1e-3, rtol=0)
+    assert out1["tokens"][0] == int(np.argmax(models.tiny_rows(fx["logits"], 4, 1)))
+    first.close()
+    last.close()
+
+
+def test_boundary_encode_is_the_reference_codec():
+    """Non-final stage output bits equal the oracle's F16 RNE of the stage's F32 hidden."""
+    _say("boundary codec")
+    first = tiny_stage("f32", 0, 1, True, False)
+    s0 = first.allocate(32)
+    out = first.execute([capi.item(s0, 5, 0)], token_ids=[1, 4, 2, 8, 3], trace=True)
+    assert np.array_equal(out["boundary"], oracle.f16_encode(out["trace"][0]))
+    first.close()
+
+
+def _oracle_generate(shape, prompt, steps, seed=0, norm_sigma=0.1):
+    st = oracle.OracleStage(models.synthetic_stage(shape, seed=seed, norm_sigma=norm_sigma))
+    return st.generate(prompt, steps)
+
+
+@pytest.mark.parametrize("execution", ["f32", "f16"])
+def test_tiny_llama_greedy_matches_oracle(execution):
+    _say("tiny-llama greedy", execution)
+    shape = synthetic.TINY_LLAMA
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, shape.vocab, 8).tolist()
+    expect, expect_logits = _oracle_generate(shape, prompt, 16)
+    cfg = model.stage_config(shape, execution=execution, kv_cache_bytes=8 << 20, max_sequences=4,
+                             max_pass_rows=64)
+    st = capi.Stage(cfg)
+    model.synthesize(st, shape, seed=0, norm_sigma=0.1)
+    seq = st.allocate(64)
+    out = st.execute([capi.item(seq, 8, 0)], token_ids=prompt, want_logits=True)
+    tokens, logits = [int(out["tokens"][0])], [out["logits"][0]]
+    for step in range(16):
+        out = st.execute([capi.item(seq, 1, 8 + step)], token_ids=[tokens[-1]], want_logits=True)
+        tokens.append(int(out["tokens"][0]))
+        logits.append(out["logits"][0])
+    tol = 1e-4 if execution == "f32" else 2e-2
+    for a, b in zip(logits, expect_logits):
+        assert np.abs(a - b).max() <= tol
+    assert tokens == expect
+    st.close()
+
+
+def test_synthesized_weights_equal_uploaded_weights():
+    _say("synthesize == upload")
+    shape = synthetic.ModelShape("s", 1, 256, 512, 4, 2, 64, 1000)
+    outs = []
+    for how in ("synth", "upload"):
+        st = capi.Stage(model.stage_config(shape, kv_cache_bytes=8 << 20, max_sequences=4,
+                                           max_pass_rows=64))
+        if how == "synth":
+            model.synthesize(st, shape, seed=3, norm_sigma=0.1)
+        else:
+            tensors = {n: models.synthetic_tensor(shape, n, 3, 0.1)[1]
+                       for n in synthetic.stage_tensor_names(shape, 0, 1, True, True)}
+            model.load(st, tensors)
+        seq = st.allocate(64)
+        outs.append(st.execute([capi.item(seq, 7, 0)], token_ids=[1, 2, 3, 4, 5, 6, 7],
+                               want_logits=True, trace=True))
+        st.close()
+    assert np.array_equal(outs[0]["trace"], outs[1]["trace"])
+    assert np.array_equal(outs[0]["logits"], outs[1]["logits"])
+
+
+def _slice_shape(shape, layers):
+    return synthetic.with_layers(shape, layers)
+
+
+@pytest.mark.parametrize("execution", ["f16", "f32"])
+def test_qwen3_slice_ragged_batch_matches_oracle(execution):
+    """Qwen3-0.6B-shaped 2-layer slice, full vocabulary: a ragged pass mixing a prefill
+    chunk with decode rows of other sequences, against the oracle run per sequence."""
+    _say("qwen3-0.6b slice ragged", execution)
+    shape = _slice_shape(synthetic.QWEN3_0_6B, 2)
+    cfg = model.stage_config(shape, execution=execution, kv_cache_bytes=64 << 20,
+                             max_sequences=8, max_pass_rows=256, max_seq=4096)
+    st = capi.Stage(cfg)
+    model.synthesize(st, shape, seed=0, norm_sigma=0.1)
+    ost = oracle.OracleStage(models.synthetic_stage(shape, seed=0, norm_sigma=0.1))
+    rng = np.random.default_rng(1)
+    lengths = [37, 5, 70]
+    prompts = [rng.integers(0, shape.vocab, n).tolist() for n in lengths]
+    seqs = [st.allocate(128) for _ in lengths]
+    oseqs = [ost.allocate_sequence(128) for _ in lengths]
+    # pass 1: prefill sequences 0 and 1 whole; sequence 2 only its first 64-token chunk
+    items = [capi.item(seqs[0], 37, 0), capi.item(seqs[1], 5, 0),
+             capi.item(seqs[2], 64, 0, sample=False)]
+    ids = prompts[0] + prompts[1] + prompts[2][:64]
+    out = st.execute(items, token_ids=ids, want_logits=True, trace=True)
+    tr = []
+    ref0 = ost.execute(np.array(prompts[0], np.uint64), 0, oseqs[0], tr)
+    tr1 = []
+    ref1 = ost.execute(np.array(prompts[1], np.uint64), 0, oseqs[1], tr1)
+    oseqs[2].prefill_only = True
+    tr2 = []
+    ost.execute(np.array(prompts[2][:64], np.uint64), 0, oseqs[2], tr2)
+    oseqs[2].prefill_only = False
+    tol = 2e-2 if execution == "f16" else 1e-4
+    got = out["trace"][-1]
+    for (a, b), expect in zip(((0, 37), (37, 42), (42, 106)), (tr[1], tr1[1], tr2[1])):
+        d = got[a:b]
+        assert np.abs(d - expect).max() <= tol and cosine(d, expect) >= 0.9999
+    assert np.abs(out["logits"][0] - tr[2]).max() <= tol
+    assert np.abs(out["logits"][1] - tr1[2]).max() <= tol
+    assert cosine(out["logits"][0], tr[2]) >= 0.9999
+    if execution == "f32":
+        assert int(out["tokens"][0]) == ref0[1] and int(out["tokens"][1]) == ref1[1]
+    assert int(out["tokens"][2]) == np.iinfo(np.uint64).max
+    # pass 2: decode rows for sequences 0 and 1 (device-fed tokens) + the last chunk of 2
+    items = [capi.item(seqs[0], 1, 37, from_device=True), capi.item(seqs[1], 1, 5, from_device=True),
+             capi.item(seqs[2], 6, 64)]
+    out2 = st.execute(items, token_ids=[0, 0] + prompts[2][64:], want_logits=True)
+    tr, tr_b, tr_c = [], [], []
+    e0 = ost.execute(np.array([int(out["tokens"][0])], np.uint64), 37, oseqs[0], tr)
+    e1 = ost.execute(np.array([int(out["tokens"][1])], np.uint64), 5, oseqs[1], tr_b)
+    e2 = ost.execute(np.array(prompts[2][64:], np.uint64), 64, oseqs[2], tr_c)
+    for got_l, exp_l in zip(out2["logits"], (tr[2], tr_b[2], tr_c[2])):
+        assert np.abs(got_l - exp_l).max() <= tol
+    if execution == "f32":
+        assert [int(t) for t in out2["tokens"]] == [e0[1], e1[1], e2[1]]
+    st.close()
+
+
+def test_packing_offsets_and_kv_slots_bit_exact():
+    _say("packing layout")
+    shape = synthetic.ModelShape("p", 1, 64, 128, 4, 2, 16, 256, qk_norm=False)
+    cfg = model.stage_config(shape, kv_cache_bytes=8 << 20, max_sequences=8, max_pass_rows=512,
+                             kv_block_tokens=16, max_seq=1024)
+    st = capi.Stage(cfg)
+    model.synthesize(st, shape, seed=0)
+    seqs = [st.allocate(n) for n in (300, 20, 150, 9)]
+    rng = np.random.default_rng(5)
+    lengths = [0, 0, 0, 0]
+    for plan in ([(0, 100), (1, 7), (2, 33), (3, 9)], [(1, 1), (0, 120), (2, 1)],
+                 [(2, 1), (1, 1), (0, 1)]):
+        items = [capi.item(seqs[i], n, lengths[i], sample=False) for i, n in plan]
+        ids = rng.integers(0, 256, sum(n for _, n in plan)).tolist()
+        st.execute(items, token_ids=ids)
+        cu, pos, slots = st.last_layout(len(plan), sum(n for _, n in plan))
+        width = 64
+        table = np.full((8, width), -1, np.int32)
+        for s in seqs:
+            b, bt = st.blocks(s)
+            table[s, :len(b)] = b
+        ecu, _, epos, eslots = oracle.pack([seqs[i] for i, _ in plan],
+                                           [lengths[i] for i, _ in plan], [n for _, n in plan],
+                                           table, 16)
+        assert np.array_equal(cu, ecu.astype(np.int32))
+        assert np.array_equal(pos, epos.astype(np.int32))
+        assert np.array_equal(slots, eslots.astype(np.int32))
+        for i, n in plan:
+            lengths[i] += n
+    st.close()
+
+
+def test_decode_batch_equals_serial_execution():
+    """hLLM tests/cpp/decode_batch_contract.hpp:8-47 at T=0: ragged lengths {7,2,4,1}."""
+    _say("decode batch contract")
+    fx = models.tiny_reference()
+    del fx
+    st = tiny_stage("f32")
+    lengths = [7, 2, 4, 1]
+    reference, batched, expected = [], [], []
+    for n in lengths:
+        a, b = st.allocate(n + 1), st.allocate(n + 1)
+        for s in (a, b):
+            st.execute([capi.item(s, n, 0)], token_ids=[1] * n)
+        expected.append(int(st.execute([capi.item(a, 1, n)], token_ids=[4])["tokens"][0]))
+        reference.append(a)
+        batched.append(b)
+    out = st.execute([capi.item(b, 1, n) for b, n in zip(batched, lengths)], token_ids=[4] * 4)
+    assert [int(t) for t in out["tokens"]] == expected
+    for b, n in zip(batched, lengths):
+        assert st.length(b) == n + 1
+    st.close()
+
+
+def test_request_validation_errors():
+    _say("validation errors")
+    st = tiny_stage("f32")
+    seq = st.allocate(4)
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(seq, 1, 0)], token_ids=[11])
+    assert e.value.status == capi.INVALID_REQUEST
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(seq, 1, 3)], token_ids=[1])
+    assert e.value.status == capi.INVALID_REQUEST
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(seq, 5, 0)], token_ids=[1] * 5)
+    assert e.value.status == capi.INVALID_REQUEST
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(seq, 1, 0), capi.item(seq, 1, 0)], token_ids=[1, 1])
+    assert e.value.status == capi.INVALID_REQUEST
+    with pytest.raises(capi.StageError) as e:
+        st.allocate(33)
+    assert e.value.status == capi.INVALID_REQUEST
+    st.execute([capi.item(seq, 1, 0)], token_ids=[1])
+    assert st.length(seq) == 1
+    st.close()
+    last = tiny_stage("f32", 1, 2, False, True)
+    s1 = last.allocate(8)
+    bad = np.zeros((1, 6), np.uint16)
+    bad[0, 3] = 0x7C00
+    with pytest.raises(capi.StageError) as e:
+        last.execute([capi.item(s1, 1, 0)], boundary=bad)
+    assert e.value.status == capi.INVALID_REQUEST
+    last.close()
+
+
+def test_weight_validation_errors():
+    _say("weight validation")
+    shape = models.tiny_reference_shape()
+    w = models.tiny_reference_stage()
+    cfg = model.stage_config(shape, execution="f16", weights="f16", kv_cache_bytes=4 << 20,
+                             max_sequences=4, max_pass_rows=16)
+    st = capi.Stage(cfg)
+    with pytest.raises(capi.StageError) as e:
+        st.load_tensor("model.layers.7.mlp.up_proj.weight", w.tensors["model.layers.0.mlp.up_proj.weight"])
+    assert e.value.status == capi.INCOMPATIBLE_WORKER
+    with pytest.raises(capi.StageError) as e:
+        st.load_tensor("model.layers.0.mlp.up_proj.weight", np.zeros((3, 3), np.float32))
+    assert e.value.status == capi.INCOMPATIBLE_WORKER
+    big = w.tensors["model.layers.0.mlp.up_proj.weight"].copy()
+    big[0, 0] = 1e6  # not representable as finite F16
+    with pytest.raises(capi.StageError) as e:
+        st.load_tensor("model.layers.0.mlp.up_proj.weight", big)
+    assert e.value.status == capi.INCOMPATIBLE_WORKER
+    nan = w.tensors["model.layers.0.mlp.up_proj.weight"].copy()
+    nan[1, 1] = np.nan
+    with pytest.raises(capi.StageError) as e:
+        st.load_tensor("model.layers.0.mlp.up_proj.weight", nan)
+    assert e.value.status == capi.INCOMPATIBLE_WORKER
+    with pytest.raises(capi.StageError) as e:
+        st.finalize()
+    assert e.value.status == capi.INCOMPATIBLE_WORKER
+    st.close()
