@@ -27,7 +27,7 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_allocate", "hllm_rocm_sequence_release",
            "hllm_rocm_sequence_length", "hllm_rocm_stage_execute", "hllm_rocm_stage_submit",
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
-           "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read")
+           "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read")
 
 
 class StageError(RuntimeError):
@@ -110,6 +110,7 @@ def library() -> C.CDLL:
                                             C.POINTER(u32)]
     L.hllm_rocm_sequence_read_kv.argtypes = [vp, u32, u32, C.POINTER(C.c_float),
                                              C.POINTER(C.c_float)]
+    L.hllm_rocm_stage_read_tensor.argtypes = [vp, C.c_char_p, C.POINTER(C.c_float), u64]
     L.hllm_rocm_stage_profile.argtypes = [vp, C.c_int32]
     L.hllm_rocm_stage_profile_read.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double),
                                                C.POINTER(u64), C.POINTER(u64)]
@@ -216,6 +217,12 @@ class Stage:
         check(self.lib.hllm_rocm_sequence_read_kv(self.handle, sequence, layer,
                                                   _ptr(k, C.c_float), _ptr(v, C.c_float)))
         return k, v
+
+    def read_tensor(self, name: str, shape) -> np.ndarray:
+        out = np.zeros(shape, np.float32)
+        check(self.lib.hllm_rocm_stage_read_tensor(self.handle, name.encode(), _ptr(out, C.c_float),
+                                                   out.size))
+        return out
 
     def last_layout(self, items: int, rows: int):
         cu = np.zeros(items + 1, np.int32)

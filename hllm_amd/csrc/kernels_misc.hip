@@ -331,6 +331,7 @@ __device__ inline uint64_t splitmix64(uint64_t state) {
 // mean + n * sigma with one rounding per operation (no fused multiply-add).
 __device__ inline float synth_value(uint64_t seed, uint64_t tensor_id, uint64_t index, float mean,
                                     float sigma) {
+#pragma clang fp contract(off)
   const uint64_t base = (tensor_id << 40) + 3ull * index;
   int sum = 0;
 #pragma unroll
@@ -340,7 +341,8 @@ __device__ inline float synth_value(uint64_t seed, uint64_t tensor_id, uint64_t 
            (int)(bits >> 48);
   }
   const float n = (float)(sum + 6 - 6 * 65536) * (1.0f / 65536.0f);
-  return __fadd_rn(mean, __fmul_rn(n, sigma));
+  const float scaled = n * sigma;
+  return mean + scaled;
 }
 
 __device__ inline float source_value(const RelayoutArgs& a, uint64_t r, uint64_t c) {

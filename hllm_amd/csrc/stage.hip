@@ -129,6 +129,7 @@ class Stage {
   void sequence_blocks(uint32_t handle, int32_t* blocks, uint32_t capacity, uint32_t* count,
                        uint32_t* block_tokens);
   void read_kv(uint32_t handle, uint32_t layer, float* keys, float* values);
+  void read_tensor(const std::string& name, float* out, uint64_t elements);
   void set_profiling(bool on);
   void profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes);
 
@@ -612,6 +613,44 @@ void Stage::sequence_blocks(uint32_t handle, int32_t* blocks, uint32_t capacity,
   if (count) *count = (uint32_t)b.size();
   if (block_tokens) *block_tokens = (uint32_t)kv_.block_tokens;
   if (blocks) std::copy(b.begin(), b.begin() + std::min<size_t>(b.size(), capacity), blocks);
+}
+
+void Stage::read_tensor(const std::string& name, float* out, uint64_t elements) {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  auto it = targets_.find(name);
+  if (it == targets_.end() || !it->second.loaded) fail(HLLM_INVALID_REQUEST, "unknown or unloaded tensor: " + name);
+  const Target& t = it->second;
+  const uint64_t rows = t.shape.size() == 2 ? t.shape[0] : 1;
+  const uint64_t cols = t.shape.size() == 2 ? t.shape[1] : t.shape[0];
+  if (elements != rows * cols) fail(HLLM_INVALID_REQUEST, "element count mismatch");
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  if (!t.matrix) {
+    HIP_CHECK(hipMemcpy(out, t.vector->ptr, elements * sizeof(float), hipMemcpyDeviceToHost));
+    return;
+  }
+  const Matrix& m = *t.matrix;
+  std::vector<uint16_t> hi(m.rows_padded * m.cols_padded), lo;
+  HIP_CHECK(hipMemcpy(hi.data(), m.hi.ptr, hi.size() * 2, hipMemcpyDeviceToHost));
+  if (m.lo.ptr) {
+    lo.resize(hi.size());
+    HIP_CHECK(hipMemcpy(lo.data(), m.lo.ptr, lo.size() * 2, hipMemcpyDeviceToHost));
+  }
+  auto half_to_float = [](uint16_t b) {
+    _Float16 h;
+    std::memcpy(&h, &b, 2);
+    return (float)h;
+  };
+  for (uint64_t r = 0; r < rows; ++r) {
+    uint64_t dr = t.row_offset + r;
+    if (t.row_mode == 1) dr = t.row_offset + (r / 32) * 64 + (r % 32);
+    if (t.row_mode == 2) dr = t.row_offset + (r / 32) * 64 + 32 + (r % 32);
+    for (uint64_t c = 0; c < cols; ++c) {
+      const uint64_t at = flayout_index(dr, c, m.cols_padded);
+      float v = half_to_float(hi[at]);
+      if (!lo.empty()) v += half_to_float(lo[at]) * kLoUnscale;
+      out[r * cols + c] = v;
+    }
+  }
 }
 
 void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values) {
@@ -1101,6 +1140,13 @@ hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, 
 hllm_status hllm_rocm_sequence_blocks(hllm_rocm_stage* stage, uint32_t sequence, int32_t* blocks,
                                       uint32_t capacity, uint32_t* count, uint32_t* block_tokens) {
   return guarded([&] { impl(stage).sequence_blocks(sequence, blocks, capacity, count, block_tokens); });
+}
+
+hllm_status hllm_rocm_stage_read_tensor(hllm_rocm_stage* stage, const char* name, float* out, uint64_t elements) {
+  return guarded([&] {
+    if (!name || !out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).read_tensor(name, out, elements);
+  });
 }
 
 hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer, float* keys,

@@ -174,6 +174,9 @@ hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, 
                                         int32_t* row_slots);
 hllm_status hllm_rocm_sequence_blocks(hllm_rocm_stage* stage, uint32_t sequence, int32_t* blocks,
                                       uint32_t capacity, uint32_t* count, uint32_t* block_tokens);
+/* One loaded tensor back as row-major F32 (hi + lo parts recombined), for loader tests. */
+hllm_status hllm_rocm_stage_read_tensor(hllm_rocm_stage* stage, const char* name, float* out,
+                                        uint64_t elements);
 hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer,
                                        float* keys, float* values);
 

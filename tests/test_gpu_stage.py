@@ -138,6 +138,33 @@ def test_tiny_llama_greedy_matches_oracle(execution):
     st.close()
 
 
+@pytest.mark.parametrize("dtype,execution", [("f16", "f16"), ("f16", "f32"), ("f32", "f32")])
+def test_synthesized_and_uploaded_tensors_equal_the_oracle_bitwise(dtype, execution):
+    """Device generator == host generator, and the F-layout relayout round-trips every
+    element (including gate/up interleave and fused q/k/v rows). F16-resident weights are
+    bit-exact; F32-resident weights are held as hi + lo/2048 F16 parts, which keeps about
+    22 significand bits: relative error <= 2^-20."""
+    _say("tensor readback", dtype, execution)
+    from dataclasses import replace
+    shape = replace(synthetic.ModelShape("s", 1, 96, 80, 3, 1, 32, 300), dtype=dtype)
+    names = synthetic.stage_tensor_names(shape, 0, 1, True, True)
+    for how in ("synth", "upload"):
+        st = capi.Stage(model.stage_config(shape, execution=execution, kv_cache_bytes=4 << 20,
+                                           max_sequences=2, max_pass_rows=32))
+        if how == "synth":
+            model.synthesize(st, shape, seed=7, norm_sigma=0.1)
+        else:
+            model.load(st, {n: models.synthetic_tensor(shape, n, 7, 0.1)[1] for n in names})
+        for n in names:
+            expect = models.synthetic_tensor(shape, n, 7, 0.1)[0]
+            got = st.read_tensor(n, expect.shape)
+            if execution == "f32" and dtype == "f32":
+                assert np.all(np.abs(got - expect) <= np.abs(expect) * 2.0 ** -20), (how, n)
+            else:
+                assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), (how, n)
+        st.close()
+
+
 def test_synthesized_weights_equal_uploaded_weights():
     _say("synthesize == upload")
     shape = synthetic.ModelShape("s", 1, 256, 512, 4, 2, 64, 1000)
