@@ -1,0 +1,392 @@
+"""Benchmark of the MI355X decoder stage worker on its headline workload.
+
+Workload (one GPU): a Qwen3-4B-shaped dense decoder (36 layers, hidden 2560, 32/8 heads,
+head_dim 128, SwiGLU 9728, vocabulary 151936, QK-norm, tied head) with seeded
+random-init F16 weights, serving 64 concurrent requests by continuous batching: Poisson
+arrivals, prompt lengths lognormal (median 256, sigma 1, clipped to [16, 2048]), output
+lengths uniform in [64, 256], prefill in chunks of at most 512 tokens per pass mixed with
+the decode rows of every running request. One step = one pass of the stage over one such
+ragged batch; the value is output (sampled) tokens per second over the timed steps.
+
+Also measured: pure decode passes of 64 rows (HBM bytes / step time against 8 TB/s),
+512-token prefill passes (FLOPs / time against 2.5 PFLOP/s dense F16), p50/p99 step
+latency, per-kernel HIP-event roofline of the dominant kernel, and the reference CPU
+worker's arithmetic (oracle/_ref, one thread) timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from hllm_amd import capi, model, synthetic  # noqa: E402
+
+METRIC = "Qwen3-4B F16 output tok/s @64 concurrent; decode HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def log(*what):
+    print("[bench]", *what, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ workload
+
+class Request:
+    __slots__ = ("prompt", "out_len", "seq", "fed", "generated", "length", "arrival")
+
+    def __init__(self, prompt, out_len, arrival):
+        self.prompt, self.out_len, self.arrival = prompt, out_len, arrival
+        self.seq, self.fed, self.generated, self.length = -1, 0, 0, 0
+
+
+def request_stream(rng, vocab, rate_per_step):
+    step = 0.0
+    while True:
+        step += rng.exponential(1.0 / rate_per_step)
+        n = int(np.clip(round(math.exp(math.log(256.0) + rng.standard_normal())), 16, 2048))
+        prompt = rng.integers(0, vocab, n, dtype=np.uint64)
+        yield Request(prompt, int(rng.integers(64, 257)), step)
+
+
+ITEM_DTYPE = np.dtype({"names": [f for f, _ in capi.Item._fields_],
+                       "formats": [np.dtype(t) for _, t in capi.Item._fields_],
+                       "offsets": [getattr(capi.Item, f).offset for f, _ in capi.Item._fields_],
+                       "itemsize": C.sizeof(capi.Item)})
+
+
+class Engine:
+    """Continuous batching over one stage: every running request contributes one decode row
+    (its input token fed from the device), and prefilling requests share a chunk budget."""
+
+    def __init__(self, stage, concurrency, chunk, stream):
+        self.stage, self.concurrency, self.chunk, self.stream = stage, concurrency, chunk, stream
+        self.waiting = collections.deque()
+        self.active = []
+        self.clock = 0
+        self.next_req = next(stream)
+        self.items = np.zeros(concurrency + chunk, ITEM_DTYPE)
+        self.items["top_p"] = 1.0
+        self.ids = np.zeros(concurrency + chunk + 8, np.uint64)
+        self.tokens_out = np.zeros(concurrency + chunk, np.uint64)
+        self.p = capi.Pass()
+
+    def step(self):
+        while self.next_req.arrival <= self.clock:
+            self.waiting.append(self.next_req)
+            self.next_req = next(self.stream)
+        while len(self.active) < self.concurrency and self.waiting:
+            r = self.waiting.popleft()
+            r.seq = self.stage.allocate(len(r.prompt) + r.out_len)
+            self.active.append(r)
+        n = rows = 0
+        decode, prefill = [], []
+        for r in self.active:
+            if r.fed == len(r.prompt):
+                it = self.items[n]
+                it["sequence"], it["query_tokens"], it["first_position"] = r.seq, 1, r.length
+                it["flags"] = capi.ITEM_SAMPLE | capi.ITEM_TOKEN_FROM_DEVICE
+                self.ids[rows] = 0
+                n, rows = n + 1, rows + 1
+                decode.append(r)
+        budget = self.chunk
+        for r in self.active:
+            if budget == 0:
+                break
+            if r.fed < len(r.prompt):
+                take = min(budget, len(r.prompt) - r.fed)
+                it = self.items[n]
+                it["sequence"], it["query_tokens"], it["first_position"] = r.seq, take, r.length
+                it["flags"] = capi.ITEM_SAMPLE if r.fed + take == len(r.prompt) else 0
+                self.ids[rows:rows + take] = r.prompt[r.fed:r.fed + take]
+                n, rows, budget = n + 1, rows + take, budget - take
+                prefill.append((r, take))
+        p = self.p
+        p.items = n
+        p.item = self.items.ctypes.data_as(C.POINTER(capi.Item))
+        p.token_ids = self.ids.ctypes.data_as(C.POINTER(C.c_uint64))
+        p.tokens = self.tokens_out.ctypes.data_as(C.POINTER(C.c_uint64))
+        capi.check(self.stage.lib.hllm_rocm_stage_execute(self.stage.handle, C.byref(p)))
+        sampled = len(decode)
+        finished = []
+        for r in decode:
+            r.length += 1
+            r.generated += 1
+            if r.generated >= r.out_len:
+                finished.append(r)
+        for r, take in prefill:
+            r.fed += take
+            r.length += take
+            if r.fed == len(r.prompt):
+                r.generated = 1
+                sampled += 1
+        for r in finished:
+            self.stage.release(r.seq)
+            self.active.remove(r)
+        self.clock += 1
+        return sampled, rows, len(decode)
+
+    def release_all(self):
+        for r in self.active:
+            self.stage.release(r.seq)
+        self.active = []
+
+
+# ------------------------------------------------------------------ measurements
+
+def decode_bench(stage, shape, rng, rows, steps):
+    """Pure decode passes: `rows` sequences prefilled to workload-distributed lengths."""
+    lengths = [int(np.clip(round(math.exp(math.log(256.0) + rng.standard_normal())), 16, 2048))
+               for _ in range(rows)]
+    seqs = [stage.allocate(n + steps + 1) for n in lengths]
+    for s, n in zip(seqs, lengths):  # untimed prefill, 512-token chunks
+        pos = 0
+        while pos < n:
+            take = min(512, n - pos)
+            stage.execute([capi.item(s, take, pos, sample=pos + take == n)],
+                          token_ids=rng.integers(0, shape.vocab, take).tolist())
+            pos += take
+    items = np.zeros(rows, ITEM_DTYPE)
+    items["top_p"] = 1.0
+    items["sequence"] = seqs
+    items["query_tokens"] = 1
+    items["flags"] = capi.ITEM_SAMPLE | capi.ITEM_TOKEN_FROM_DEVICE
+    ids = np.zeros(rows, np.uint64)
+    out = np.zeros(rows, np.uint64)
+    p = capi.Pass()
+    p.items = rows
+    p.item = items.ctypes.data_as(C.POINTER(capi.Item))
+    p.token_ids = ids.ctypes.data_as(C.POINTER(C.c_uint64))
+    p.tokens = out.ctypes.data_as(C.POINTER(C.c_uint64))
+    ctx = np.array(lengths, np.int64)
+    times, kv_read = [], 0
+    for i in range(steps + 4):
+        if i == steps:  # per-kernel HIP-event timing in 4 extra, untimed passes
+            stage.profile("gemm_,attention")
+        items["first_position"] = ctx
+        t0 = time.perf_counter()
+        capi.check(stage.lib.hllm_rocm_stage_execute(stage.handle, C.byref(p)))
+        if i < steps:
+            times.append(time.perf_counter() - t0)
+            kv_read += int((ctx + 1).sum())
+        ctx += 1
+    fam = {f: stage.profile_read(f) for f in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
+                                              "gemm_lm_head", "attention")}
+    stage.profile(None)
+    for s in seqs:
+        stage.release(s)
+    kv_tok = shape.kv_bytes_per_token()
+    weights = shape.layers * shape.layer_weight_bytes() + shape.vocab * shape.hidden * 2
+    total_bytes = steps * (weights + rows * kv_tok) + kv_read * kv_tok
+    elapsed = sum(times)
+    gbs = total_bytes / elapsed / 1e9
+    return {"rows": rows, "steps": steps, "mean_context": float(np.mean(lengths) + steps / 2),
+            "ms_per_step": 1e3 * elapsed / steps, "tok_s": rows * steps / elapsed,
+            "bytes_per_step": total_bytes / steps, "hbm_gb_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "kernels": {f: {"ms_per_launch": v[0] / max(v[1], 1), "launches": v[1],
+                            "gb_s": (v[2] / v[1]) / (v[0] / v[1] * 1e-3) / 1e9 if v[1] else 0.0}
+                        for f, v in fam.items()}}
+
+
+def prefill_bench(stage, shape, rng, past, reps):
+    """512-token prefill chunks (no sampling) at context offset `past`: MFMA utilisation."""
+    flops_linear = 2 * 512 * shape.layers * (shape.layer_weight_bytes() // 2)
+    pairs = sum(past + i + 1 for i in range(512))
+    flops_attn = 4 * shape.heads * shape.head_dim * shape.layers * pairs
+    times = []
+    for _ in range(reps):
+        s = stage.allocate(past + 512)
+        pos = 0
+        while pos < past:
+            take = min(512, past - pos)
+            stage.execute([capi.item(s, take, pos, sample=False)],
+                          token_ids=rng.integers(0, shape.vocab, take).tolist())
+            pos += take
+        ids = rng.integers(0, shape.vocab, 512).tolist()
+        t0 = time.perf_counter()
+        stage.execute([capi.item(s, 512, past, sample=False)], token_ids=ids)
+        times.append(time.perf_counter() - t0)
+        stage.release(s)
+    t = float(np.median(times))
+    tflops = (flops_linear + flops_attn) / t / 1e12
+    return {"past": past, "ms": 1e3 * t, "tflop": (flops_linear + flops_attn) / 1e12,
+            "tflops": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+
+
+def cpu_baseline(shape, mean_context):
+    """The reference CPU worker's own arithmetic (oracle/_ref, compiled from its sources),
+    one thread: one decode step of one Qwen3-4B layer at the workload's mean context, and
+    the final norm + LM head over one eighth of the vocabulary; the per-token time is
+    36 layer steps + 8 head slices (an extrapolation from the measured sample)."""
+    import oracle  # the CPU-baseline leg runs the reference's arithmetic as the baseline
+    R = oracle.ref()
+    kind = "reference"
+    if R is None:
+        return None
+    cfg = oracle.Config(shape.hidden, shape.intermediate, shape.heads, shape.kv_heads,
+                        shape.head_dim, shape.max_seq, shape.eps, shape.theta, int(shape.qk_norm))
+    names = synthetic.LAYER_TENSORS
+    arrays = []
+    for n in names:
+        tid, dims, mean, sigma = synthetic.tensor_spec(shape, f"model.layers.0.{n}")
+        bits = oracle.synth_f16(0, tid, int(np.prod(dims)), mean, sigma)
+        arrays.append(oracle.f16_decode(bits))
+    layer = R.ref_layer_create(C.byref(cfg), *[a.ctypes.data for a in arrays])
+    width = shape.kv_heads * shape.head_dim
+    ctx = int(mean_context)
+    cache = R.ref_cache_create(ctx + 4, shape.kv_heads, shape.head_dim)
+    rng = np.random.default_rng(0)
+    kv = rng.standard_normal((2, ctx, width)).astype(np.float32)
+    assert R.ref_cache_append(cache, 0, np.ascontiguousarray(kv[0]), np.ascontiguousarray(kv[1]),
+                              ctx, width) == 0
+    x = rng.standard_normal((1, shape.hidden)).astype(np.float32)
+    out = np.empty_like(x)
+    layer_times = []
+    for i in range(2):
+        t0 = time.perf_counter()
+        assert R.ref_transformer_layer(C.byref(cfg), layer, x, 1, ctx + i, cache, out) == 0
+        layer_times.append(time.perf_counter() - t0)
+    R.ref_layer_destroy(layer)
+    R.ref_cache_destroy(cache)
+    del arrays
+    slice_rows = shape.vocab // 8
+    tid, _, mean, sigma = synthetic.tensor_spec(shape, "model.embed_tokens.weight")
+    head = oracle.f16_decode(oracle.synth_f16(0, tid, slice_rows * shape.hidden, mean, sigma))
+    norm = np.ones(shape.hidden, np.float32)
+    logits = np.empty((1, slice_rows), np.float32)
+    t0 = time.perf_counter()
+    assert R.ref_final_logits(x, 1, shape.hidden, norm, head, slice_rows, shape.eps, logits) == 0
+    t_head = (time.perf_counter() - t0) * 8
+    t_layer = min(layer_times)
+    per_token = shape.layers * t_layer + t_head
+    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": 1, "kind": kind,
+            "sample": f"reference CPU worker arithmetic (cpp/src/cpu/llama.cpp via oracle/_ref), "
+                      f"1 thread: one Qwen3-4B layer decode step at context {ctx} "
+                      f"({1e3 * t_layer:.0f} ms, x36) + final norm/LM head over 1/8 of the "
+                      f"vocabulary ({1e3 * t_head / 8:.0f} ms, x8); extrapolated per-token time "
+                      f"{per_token:.2f} s at batch 1; host nproc {os.cpu_count()}",
+            "ms_per_token": 1e3 * per_token}
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=120)
+    ap.add_argument("--concurrency", type=int, default=64)
+    ap.add_argument("--chunk", type=int, default=512)
+    ap.add_argument("--rate", type=float, default=1.0, help="Poisson arrivals per step")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=0, help="truncate the model (debug only)")
+    ap.add_argument("--decode-steps", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-extras", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        sys.exit("bench.py measures one GPU: the stage worker runs the whole model (or one "
+                 "pipeline stage's share) on a single MI355X; multi-GPU runs are not part of "
+                 "this build")
+
+    shape = synthetic.QWEN3_4B
+    if args.layers:
+        shape = synthetic.with_layers(shape, args.layers)
+    rows_max = args.chunk + args.concurrency
+    cfg = model.stage_config(shape, execution="f16", kv_cache_bytes=48 << 30,
+                             max_sequences=4 * args.concurrency,
+                             max_pass_rows=((rows_max + 127) // 128) * 128, max_seq=4096)
+    t0 = time.perf_counter()
+    stage = capi.Stage(cfg)
+    model.synthesize(stage, shape, seed=args.seed, norm_sigma=0.0)
+    log(f"stage ready in {time.perf_counter() - t0:.1f}s; weights "
+        f"{stage.weight_memory().device_bytes / 1e9:.2f} GB")
+
+    rng = np.random.default_rng(args.seed)
+    engine = Engine(stage, args.concurrency, args.chunk,
+                    request_stream(np.random.default_rng(args.seed + 1), shape.vocab, args.rate))
+    for i in range(args.warmup):
+        if i == max(0, args.warmup - 20):
+            stage.profile("*")
+        engine.step()
+    families = ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "gemm_lm_head", "attention",
+                "norm", "rope_append", "embed", "argmax", "pack")
+    prof = {f: stage.profile_read(f) for f in families}
+    dominant = max(prof, key=lambda f: prof[f][0])
+    log("warmup kernel time (ms) by family:",
+        {f: round(v[0], 2) for f, v in sorted(prof.items(), key=lambda kv: -kv[1][0])})
+    log(f"active {len(engine.active)} waiting {len(engine.waiting)}; dominant kernel {dominant}")
+
+    stage.profile(dominant)
+    step_ms, tokens, rows_total, decode_rows = [], 0, 0, 0
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        t0 = time.perf_counter()
+        s, r, d = engine.step()
+        step_ms.append(1e3 * (time.perf_counter() - t0))
+        tokens += s
+        rows_total += r
+        decode_rows += d
+    elapsed = time.perf_counter() - t_start
+    dom_ms, dom_n, dom_bytes = stage.profile_read(dominant)
+    stage.profile(None)
+    log(f"timed {args.steps} steps in {elapsed:.3f}s: {tokens} tokens, {rows_total} rows "
+        f"({decode_rows} decode rows)")
+    engine.release_all()
+
+    avg_launch_s = dom_ms / max(dom_n, 1) * 1e-3
+    achieved = (dom_bytes / max(dom_n, 1)) / avg_launch_s / 1e9 if dom_n else 0.0
+    result = {
+        "metric": METRIC,
+        "value": tokens / elapsed,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * elapsed / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random-init weights, random prompt token IDs)",
+        "config": {"workload": f"{shape.name} continuous batching: {args.concurrency} concurrent, "
+                               f"Poisson arrivals {args.rate}/step, prompts lognormal(median 256, "
+                               f"sigma 1) in [16,2048], outputs U[64,256], chunked prefill "
+                               f"{args.chunk} mixed with decode rows",
+                   "concurrency": args.concurrency, "chunk": args.chunk,
+                   "rows_per_step": rows_total / args.steps,
+                   "decode_rows_per_step": decode_rows / args.steps},
+        "latency_ms": {"p50": float(np.percentile(step_ms, 50)),
+                       "p99": float(np.percentile(step_ms, 99))},
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "launches": dom_n,
+                     "avg_launch_us": avg_launch_s * 1e6,
+                     "algorithmic_bytes_per_launch": dom_bytes / max(dom_n, 1)},
+    }
+    if not args.skip_extras:
+        result["decode"] = decode_bench(stage, shape, rng, args.concurrency, args.decode_steps)
+        log("decode:", json.dumps({k: v for k, v in result["decode"].items() if k != "kernels"}))
+        result["prefill"] = [prefill_bench(stage, shape, rng, past, 3) for past in (0, 1536)]
+        log("prefill:", json.dumps(result["prefill"]))
+    stage.close()
+    if not args.no_cpu_baseline:
+        mean_ctx = result.get("decode", {}).get("mean_context", 483.0)
+        result["cpu_baseline"] = cpu_baseline(synthetic.QWEN3_4B, mean_ctx)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

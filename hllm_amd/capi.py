@@ -111,7 +111,7 @@ def library() -> C.CDLL:
     L.hllm_rocm_sequence_read_kv.argtypes = [vp, u32, u32, C.POINTER(C.c_float),
                                              C.POINTER(C.c_float)]
     L.hllm_rocm_stage_read_tensor.argtypes = [vp, C.c_char_p, C.POINTER(C.c_float), u64]
-    L.hllm_rocm_stage_profile.argtypes = [vp, C.c_int32]
+    L.hllm_rocm_stage_profile.argtypes = [vp, C.c_char_p]
     L.hllm_rocm_stage_profile_read.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double),
                                                C.POINTER(u64), C.POINTER(u64)]
     for name in EXPORTS:
@@ -276,8 +276,9 @@ class Stage:
         return out
 
     # --------------------------------------------------------------- profiling
-    def profile(self, enable: bool) -> None:
-        check(self.lib.hllm_rocm_stage_profile(self.handle, int(enable)))
+    def profile(self, families: str | None) -> None:
+        """Time the named kernel families ("*" = all, None = off)."""
+        check(self.lib.hllm_rocm_stage_profile(self.handle, families.encode() if families else None))
 
     def profile_read(self, family: str):
         ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()

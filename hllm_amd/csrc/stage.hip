@@ -130,7 +130,7 @@ class Stage {
                        uint32_t* block_tokens);
   void read_kv(uint32_t handle, uint32_t layer, float* keys, float* values);
   void read_tensor(const std::string& name, float* out, uint64_t elements);
-  void set_profiling(bool on);
+  void set_profiling(const std::string& families);
   void profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes);
 
  private:
@@ -195,6 +195,7 @@ class Stage {
   uint64_t pending_rows_ = 0;
 
   bool profiling_ = false;
+  std::vector<std::string> profile_filter_;
   std::map<std::string, Profile> profiles_;
   std::vector<hipEvent_t> event_pool_;
 };
@@ -695,7 +696,13 @@ void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values)
 
 template <typename F>
 void Stage::timed(const char* family, uint64_t bytes, F&& launch) {
-  if (!profiling_) {
+  bool selected = false;
+  if (profiling_) {
+    for (const auto& prefix : profile_filter_) {
+      if (prefix == "*" || std::strncmp(family, prefix.c_str(), prefix.size()) == 0) selected = true;
+    }
+  }
+  if (!selected) {
     launch();
     return;
   }
@@ -718,13 +725,20 @@ void Stage::timed(const char* family, uint64_t bytes, F&& launch) {
   p.bytes += bytes;
 }
 
-void Stage::set_profiling(bool on) {
+void Stage::set_profiling(const std::string& families) {
   std::lock_guard<std::mutex> lock(pass_mutex_);
   HIP_CHECK(hipStreamSynchronize(stream_));
   for (auto& [name, p] : profiles_)
     for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
   profiles_.clear();
-  profiling_ = on;
+  profile_filter_.clear();
+  size_t start = 0;
+  while (start <= families.size()) {
+    const size_t end = std::min(families.find(',', start), families.size());
+    if (end > start) profile_filter_.push_back(families.substr(start, end - start));
+    start = end + 1;
+  }
+  profiling_ = !profile_filter_.empty();
 }
 
 void Stage::profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes) {
@@ -1157,8 +1171,8 @@ hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence
   });
 }
 
-hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, int32_t enable) {
-  return guarded([&] { impl(stage).set_profiling(enable != 0); });
+hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, const char* families) {
+  return guarded([&] { impl(stage).set_profiling(families ? families : ""); });
 }
 
 hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family, double* milliseconds,

@@ -180,9 +180,11 @@ hllm_status hllm_rocm_stage_read_tensor(hllm_rocm_stage* stage, const char* name
 hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer,
                                        float* keys, float* values);
 
-/* Profiling hooks for benchmarks: HIP events around every launch of one kernel family
- * ("gemm_decode", "attention", ...), summed per family since the last reset. */
-hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, int32_t enable);
+/* Profiling hooks for benchmarks: HIP events on the stage's stream around every launch of
+ * the kernel families named in `families` (comma-separated prefixes such as
+ * "gemm_gate_up,attention"; "*" = all; NULL or "" = off), with the algorithmic bytes of
+ * each launch; read back as sums per family (a trailing '*' matches a prefix). */
+hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, const char* families);
 hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family,
                                          double* milliseconds, uint64_t* launches,
                                          uint64_t* bytes);

@@ -147,6 +147,7 @@ def ref() -> C.CDLL | None:
         R.ref_cache_length.restype = _sz
         R.ref_cache_length.argtypes = [C.c_void_p]
         R.ref_cache_read.argtypes = [C.c_void_p, _f32p, _f32p]
+        R.ref_cache_append.argtypes = [C.c_void_p, _sz, _f32p, _f32p, _sz, _sz]
         R.ref_transformer_layer.argtypes = [C.POINTER(Config), C.c_void_p, _f32p, _sz, _sz,
                                             C.c_void_p, _f32p]
         R.ref_rms_norm.argtypes = [_f32p, _sz, _sz, _f32p, C.c_float, _f32p]

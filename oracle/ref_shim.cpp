@@ -108,6 +108,18 @@ void ref_cache_read(const void* opaque, float* keys, float* values) {
       }
 }
 
+// LayerKvCache::append with given K/V rows (positions first_position..+rows).
+int ref_cache_append(void* cache, std::size_t first_position, const float* keys,
+                     const float* values, std::size_t rows, std::size_t width) {
+  try {
+    static_cast<LayerKvCache*>(cache)->append(first_position, matrix(keys, rows, width),
+                                              matrix(values, rows, width));
+    return 0;
+  } catch (const std::exception& e) {
+    return status_of(e);
+  }
+}
+
 int ref_transformer_layer(const RefConfig* c, const void* layer, const float* input,
                           std::size_t rows, std::size_t first_position, void* cache,
                           float* output) {
