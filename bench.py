@@ -113,6 +113,9 @@ class Engine:
                 self.ids[rows:rows + take] = r.prompt[r.fed:r.fed + take]
                 n, rows, budget = n + 1, rows + take, budget - take
                 prefill.append((r, take))
+        if n == 0:  # nothing has arrived yet: an idle step launches nothing
+            self.clock += 1
+            return 0, 0, 0
         p = self.p
         p.items = n
         p.item = self.items.ctypes.data_as(C.POINTER(capi.Item))
@@ -150,7 +153,7 @@ def decode_bench(stage, shape, rng, rows, steps):
     """Pure decode passes: `rows` sequences prefilled to workload-distributed lengths."""
     lengths = [int(np.clip(round(math.exp(math.log(256.0) + rng.standard_normal())), 16, 2048))
                for _ in range(rows)]
-    seqs = [stage.allocate(n + steps + 1) for n in lengths]
+    seqs = [stage.allocate(n + steps + 8) for n in lengths]
     for s, n in zip(seqs, lengths):  # untimed prefill, 512-token chunks
         pos = 0
         while pos < n:

@@ -1,23 +1,35 @@
 // Ragged causal GQA attention over the paged KV cache.
 //
-// Work item = (packed row, KV head, context split). The G = Q/K query heads that share a
-// KV head are handled together so every K/V element is read once per row. A split walks
-// its positions in tiles of 256: K rows are scored by one thread each (G dot products),
-// the tile's softmax statistics are reduced per head, and the value sum is accumulated by
-// threads that own (head, dimension) pairs, reading V rows coalesced. Online softmax keeps
-// (max, sum, acc) across tiles; the combine kernel merges splits and writes the
-// O-projection operand (F-layout, hi and optional lo parts).
+// F16 KV, head_dim in {64, 128, 256}: MFMA flash attention. A work item is a block of up
+// to 64 query vectors (query rows x the G query heads that share one KV head) against one
+// split of its key range, for one KV head. Scores are computed transposed, S^T = K Q^T
+// (v_mfma_f32_16x16x32_f16 with a cached key fragment as the A operand, loaded straight
+// from the paged cache), so that each lane holds four positions of one query vector; the
+// probabilities of 32 positions then form the B operand of O^T = V^T P directly in
+// registers: both operands list the positions in the same k-slot order (the values are
+// stored transposed per block, so V^T rows load as 8-byte pieces). Online softmax runs in
+// F32 per query vector. Blocks of at most 16 vectors (decode rows) let the four waves
+// interleave 32-key tiles and merge through LDS; larger blocks give each wave 16 vectors.
 //
-// Scores, softmax and accumulation are F32 (cpp/src/cpu/llama.cpp:67-112 semantics,
-// cpp/src/cuda/stage.cpp:291-300: F32 scores and softmax); K/V are F16 or F32.
+// F32 KV (F32 execution) or other head dims: the F32 VALU kernel, one work item per
+// (row, KV head, split), one thread per key for the scores and coalesced value reads.
+//
+// Splits of one query block are merged by the combine kernel. Scores, softmax and
+// accumulation are F32 (cpp/src/cpu/llama.cpp:67-112; cpp/src/cuda/stage.cpp:291-300).
 #include "kernels.hpp"
 
 namespace hllm_rocm {
 namespace {
 
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
 constexpr int kTile = 256;
 constexpr int kMaxPairs = 8;  // (head, dim) pairs per thread: G * D <= 2048
+
+__device__ inline floatx4 mfma(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 __device__ inline float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -27,8 +39,186 @@ __device__ inline float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// exp(m - reference) with the empty-softmax convention: a -inf maximum contributes nothing.
+__device__ inline float rescale(float m, float reference) {
+  return m == -INFINITY ? 0.0f : expf(m - reference);
+}
 
-__device__ inline int split_length(int ctx, int max_splits, int unit) {
+__device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int split) {
+  return a.partial + (((size_t)row * a.q_heads + qh) * a.max_splits + split) * (a.head_dim + 2);
+}
+
+// ---------------------------------------------------------------- MFMA flash attention
+
+template <int D>
+__global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs a) {
+  constexpr int KK = D / 32;  // 32-wide chunks of the QK contraction
+  constexpr int DF = D / 16;  // 16-row fragments of O^T
+  extern __shared__ float smem[];
+  const AttnWork w = a.work[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int G = a.q_heads / a.kv_heads;
+  const int nvec = w.rows * G;
+  const bool split_keys = nvec <= 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int quad = lane >> 4, col = lane & 15;
+  const int vf = split_keys ? 0 : wave;
+  const int v = vf * 16 + col;
+  const bool v_ok = v < nvec;
+  const int vr = v / G, vg = v - vr * G;
+  const int my_pos = w.position0 + vr;
+  if (!split_keys && vf * 16 >= nvec) return;  // no __syncthreads on this path
+  const int seq = a.items[w.item].sequence;
+  const int32_t* table = a.block_table + (size_t)seq * a.table_width;
+  const int bt = a.kv.block_tokens, KVH = a.kv_heads;
+  const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
+
+  // Q^T as the B operand (1/sqrt(D) folded in): lane holds Q[v][32 kk + 8 quad + j].
+  half8 qf[KK];
+  {
+    const float* qrow = a.q + ((size_t)(w.row0 + (v_ok ? vr : 0)) * a.q_heads + kvh * G + vg) * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        qf[kk][j] = v_ok ? to_half(qrow[32 * kk + 8 * quad + j] * a.scale) : (_Float16)0.0f;
+  }
+  floatx4 o[DF];
+#pragma unroll
+  for (int df = 0; df < DF; ++df) o[df] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  const int stride = split_keys ? 4 : 1;
+  for (int t = w.key_begin + 32 * (split_keys ? wave : 0); t < w.key_end; t += 32 * stride) {
+    const int logical = t / bt;
+    const uint64_t blk = (uint64_t)table[logical];
+    const int off = t - logical * bt;
+    const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
+    floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const half8 k0 = *reinterpret_cast<const half8*>(kb + (size_t)col * D + 32 * kk + 8 * quad);
+      const half8 k1 = *reinterpret_cast<const half8*>(kb + (size_t)(16 + col) * D + 32 * kk + 8 * quad);
+      s0 = mfma(k0, qf[kk], s0);
+      s1 = mfma(k1, qf[kk], s1);
+    }
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p0 = t + 4 * quad + i, p1 = t + 16 + 4 * quad + i;
+      sc[i] = (v_ok && p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
+      sc[4 + i] = (v_ok && p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+    }
+    float tmax = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sc[i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m, tmax);
+    const float base = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = rescale(m, base);
+    half8 pf;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = sc[i] == -INFINITY ? 0.0f : expf(sc[i] - base);
+      psum += p;
+      pf[i] = to_half(p);
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+    m = m_new;
+    const _Float16* vb = pool + (((blk * 2 + 1) * KVH + kvh) * D) * bt + off;
+    // A tile that runs past the key range reads cache slots no pass has written: zero
+    // them, since a zero probability does not cancel a non-finite value.
+    const bool tail = t + 32 > w.key_end;
+#pragma unroll
+    for (int df = 0; df < DF; ++df) {
+      o[df][0] *= alpha;
+      o[df][1] *= alpha;
+      o[df][2] *= alpha;
+      o[df][3] *= alpha;
+      const _Float16* vrow = vb + (size_t)(16 * df + col) * bt;
+      const half4 a0 = *reinterpret_cast<const half4*>(vrow + 4 * quad);
+      const half4 a1 = *reinterpret_cast<const half4*>(vrow + 16 + 4 * quad);
+      half8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      if (tail) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (t + 4 * quad + i >= w.key_end) av[i] = (_Float16)0.0f;
+          if (t + 16 + 4 * quad + i >= w.key_end) av[4 + i] = (_Float16)0.0f;
+        }
+      }
+      o[df] = mfma(av, pf, o[df]);
+    }
+  }
+
+  float m_fin = m, l_fin = l;
+  if (split_keys) {
+    // Merge the four waves' partial softmax states (vectors 0..15) through LDS.
+    float* sm_m = smem;            // [4][16]
+    float* sm_l = smem + 64;       // [4][16]
+    float* sm_o = smem + 128;      // [4][D][16]
+    if (quad == 0) {
+      sm_m[wave * 16 + col] = m;
+      sm_l[wave * 16 + col] = l;
+    }
+#pragma unroll
+    for (int df = 0; df < DF; ++df)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm_o[(wave * D + 16 * df + 4 * quad + i) * 16 + col] = o[df][i];
+    __syncthreads();
+    if (wave != 0) return;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) mm = fmaxf(mm, sm_m[ww * 16 + col]);
+    float weights[4];
+    l_fin = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      weights[ww] = rescale(sm_m[ww * 16 + col], mm == -INFINITY ? 0.0f : mm);
+      l_fin += sm_l[ww * 16 + col] * weights[ww];
+    }
+    m_fin = mm;
+#pragma unroll
+    for (int df = 0; df < DF; ++df)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) s += sm_o[(ww * D + 16 * df + 4 * quad + i) * 16 + col] * weights[ww];
+        o[df][i] = s;
+      }
+  }
+  if (!v_ok) return;
+  const int row = w.row0 + vr, qh = kvh * G + vg;
+  if (w.splits == 1) {
+    const float inv = 1.0f / l_fin;
+#pragma unroll
+    for (int df = 0; df < DF; ++df) {
+      half4 y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = to_half(o[df][i] * inv);
+      const uint64_t at = flayout_index(row, (uint64_t)qh * D + 16 * df + 4 * quad, a.out_cols_padded);
+      *reinterpret_cast<half4*>(a.out_hi + at) = y;
+    }
+  } else {
+    float* out = partial_at(a, row, qh, w.split);
+#pragma unroll
+    for (int df = 0; df < DF; ++df)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[16 * df + 4 * quad + i] = o[df][i];
+    if (quad == 0) {
+      out[D] = m_fin;
+      out[D + 1] = l_fin;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- F32 VALU attention
+
+__device__ inline int valu_split_length(int ctx, int max_splits, int unit) {
   int splits = (ctx + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = (ctx + splits - 1) / splits;
@@ -36,48 +226,40 @@ __device__ inline int split_length(int ctx, int max_splits, int unit) {
 }
 
 template <typename KV>
-__global__ void __launch_bounds__(kThreads) attention_split_kernel(AttentionArgs a) {
+__global__ void __launch_bounds__(kThreads) attention_valu_kernel(AttentionArgs a) {
   const int r = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int ctx = a.row_position[r] + 1;
-  const int per = split_length(ctx, a.max_splits, a.split_unit);
+  const int per = valu_split_length(ctx, a.max_splits, a.split_unit);
   const int p0 = s * per;
   if (p0 >= ctx) return;
   const int p1 = min(ctx, p0 + per);
   const int D = a.head_dim, G = a.q_heads / a.kv_heads;
   const int seq = a.items[a.row_item[r]].sequence;
   const int32_t* table = a.block_table + (size_t)seq * a.table_width;
-  const KV* pool = static_cast<const KV*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
+  const KV* pool = static_cast<const KV*>(a.kv.pool);
   const int bt = a.kv.block_tokens;
-  const uint64_t head_stride = (uint64_t)bt * D;
 
   extern __shared__ float smem[];
   float* qs = smem;                 // [G][D]
   float* sc = qs + G * D;           // [G][kTile]
-  float* stat = sc + G * kTile;     // [G] tile max, [G] rescale
+  float* stat = sc + G * kTile;     // [G] tile max, [G] tile sum
   const int tid = threadIdx.x;
-  for (int e = tid; e < G * D; e += kThreads) {
-    qs[e] = a.q[((size_t)r * a.q_heads + kvh * G) * D + e];
-  }
-  // Thread-owned (head, dim) pairs: dim = tid % D, heads tid / D + k * (256 / D).
+  for (int e = tid; e < G * D; e += kThreads) qs[e] = a.q[((size_t)r * a.q_heads + kvh * G) * D + e];
   const int my_d = tid % D;
   const int h_first = tid / D, h_step = kThreads / D > 0 ? kThreads / D : 1;
-  float acc[kMaxPairs];
-#pragma unroll
-  for (int k = 0; k < kMaxPairs; ++k) acc[k] = 0.0f;
-  float run_max[kMaxPairs], run_sum[kMaxPairs];
+  float acc[kMaxPairs], run_max[kMaxPairs], run_sum[kMaxPairs];
 #pragma unroll
   for (int k = 0; k < kMaxPairs; ++k) {
+    acc[k] = 0.0f;
     run_max[k] = -INFINITY;
     run_sum[k] = 0.0f;
   }
   __syncthreads();
-
   for (int t0 = p0; t0 < p1; t0 += kTile) {
     const int n = min(kTile, p1 - t0);
     if (tid < n) {
       const int p = t0 + tid;
-      const KV* k = pool + ((uint64_t)table[p / bt] * 2 * a.kv_heads + kvh) * head_stride +
-                    (uint64_t)(p % bt) * D;
+      const KV* k = pool + kv_key_index(a.kv, a.layer, (uint64_t)table[p / bt], p % bt, kvh, 0);
       float dots[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) dots[g] = 0.0f;
@@ -92,33 +274,31 @@ __global__ void __launch_bounds__(kThreads) attention_split_kernel(AttentionArgs
         if (g < G) sc[g * kTile + tid] = dots[g] * a.scale;
     }
     __syncthreads();
-    // Per-head tile maximum and exp: wave w handles heads w, w + 4, ...
     const int wave = tid >> 6, lane = tid & 63;
     for (int g = wave; g < G; g += kThreads / 64) {
-      float m = -INFINITY;
-      for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * kTile + i]);
-      m = wave_max(m);
+      float mx = -INFINITY;
+      for (int i = lane; i < n; i += 64) mx = fmaxf(mx, sc[g * kTile + i]);
+      mx = wave_max(mx);
       float sum = 0.0f;
       for (int i = lane; i < n; i += 64) {
-        const float e = expf(sc[g * kTile + i] - m);
+        const float e = expf(sc[g * kTile + i] - mx);
         sc[g * kTile + i] = e;
         sum += e;
       }
       sum = wave_sum(sum);
       if (lane == 0) {
-        stat[g] = m;
+        stat[g] = mx;
         stat[G + g] = sum;
       }
     }
     __syncthreads();
-    // Value accumulation with online rescaling.
 #pragma unroll
     for (int k = 0; k < kMaxPairs; ++k) {
       const int g = h_first + k * h_step;
-      if (tid < G * D && g < G && k * h_step * D + tid < G * D) {
+      if (tid < G * D && g < G) {
         const float tile_max = stat[g];
         const float new_max = fmaxf(run_max[k], tile_max);
-        const float old_scale = expf(run_max[k] - new_max);
+        const float old_scale = rescale(run_max[k], new_max);
         const float tile_scale = expf(tile_max - new_max);
         run_sum[k] = run_sum[k] * old_scale + stat[G + g] * tile_scale;
         run_max[k] = new_max;
@@ -126,21 +306,19 @@ __global__ void __launch_bounds__(kThreads) attention_split_kernel(AttentionArgs
         float part = 0.0f;
         for (int i = 0; i < n; ++i) {
           const int p = t0 + i;
-          const KV* v = pool + (((uint64_t)table[p / bt] * 2 + 1) * a.kv_heads + kvh) * head_stride +
-                        (uint64_t)(p % bt) * D;
-          part += sc[g * kTile + i] * (float)v[my_d];
+          const KV* v = pool + kv_value_index(a.kv, a.layer, (uint64_t)table[p / bt], p % bt, kvh, my_d);
+          part += sc[g * kTile + i] * (float)*v;
         }
         acc[k] += part * tile_scale;
       }
     }
     __syncthreads();
   }
-  const int stride = D + 2;
 #pragma unroll
   for (int k = 0; k < kMaxPairs; ++k) {
     const int g = h_first + k * h_step;
-    if (tid < G * D && g < G && k * h_step * D + tid < G * D) {
-      float* out = a.partial + (((size_t)r * a.q_heads + kvh * G + g) * a.max_splits + s) * stride;
+    if (tid < G * D && g < G) {
+      float* out = partial_at(a, r, kvh * G + g, s);
       out[my_d] = acc[k];
       if (my_d == 0) {
         out[D] = run_max[k];
@@ -150,23 +328,33 @@ __global__ void __launch_bounds__(kThreads) attention_split_kernel(AttentionArgs
   }
 }
 
-// One block per (row, query head): merge the splits, normalise, write the operand.
-__global__ void attention_combine_kernel(AttentionArgs a) {
+// ---------------------------------------------------------------- split combine
+
+// One block per (row, query head): merge the row's splits, normalise, write the operand.
+// MFMA-path rows with a single split were written by the attention kernel already.
+__global__ void attention_combine_kernel(AttentionArgs a, int mfma_path) {
   const int r = blockIdx.x, qh = blockIdx.y;
   const int D = a.head_dim;
-  const int ctx = a.row_position[r] + 1;
-  const int per = split_length(ctx, a.max_splits, a.split_unit);
-  const int splits = (ctx + per - 1) / per;
+  int splits;
+  if (mfma_path) {
+    splits = a.row_splits[r];
+    if (splits == 1) return;
+  } else {
+    const int ctx = a.row_position[r] + 1;
+    const int per = valu_split_length(ctx, a.max_splits, a.split_unit);
+    splits = (ctx + per - 1) / per;
+  }
   const int stride = D + 2;
-  const float* part = a.partial + ((size_t)r * a.q_heads + qh) * a.max_splits * stride;
+  const float* part = partial_at(a, r, qh, 0);
   float m = -INFINITY;
   for (int s = 0; s < splits; ++s) m = fmaxf(m, part[s * stride + D]);
+  const float ref = m == -INFINITY ? 0.0f : m;
   float total = 0.0f;
-  for (int s = 0; s < splits; ++s) total += part[s * stride + D + 1] * expf(part[s * stride + D] - m);
+  for (int s = 0; s < splits; ++s) total += part[s * stride + D + 1] * rescale(part[s * stride + D], ref);
   const float inv = 1.0f / total;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float v = 0.0f;
-    for (int s = 0; s < splits; ++s) v += part[s * stride + d] * expf(part[s * stride + D] - m);
+    for (int s = 0; s < splits; ++s) v += part[s * stride + d] * rescale(part[s * stride + D], ref);
     const float y = v * inv;
     const uint64_t at = flayout_index(r, (uint64_t)qh * D + d, a.out_cols_padded);
     const _Float16 hi = to_half(y);
@@ -183,18 +371,43 @@ __global__ void attention_combine_kernel(AttentionArgs a) {
   }
 }
 
+template <int D>
+void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
+  const size_t lds = (size_t)(128 + 4 * D * 16) * sizeof(float);
+  static const bool configured = [&] {
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    return true;
+  }();
+  (void)configured;
+  attention_mfma_kernel<D><<<dim3(a.work_count, a.kv_heads), kThreads, lds, stream>>>(a);
+}
+
 }  // namespace
+
+bool attention_uses_mfma(int head_dim, bool kv_f32) {
+  return !kv_f32 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
 
 void launch_attention(hipStream_t stream, const AttentionArgs& a) {
   if (a.rows <= 0) return;
-  const int G = a.q_heads / a.kv_heads;
-  const size_t lds = ((size_t)G * a.head_dim + (size_t)G * kTile + 2 * G) * sizeof(float);
-  dim3 grid(a.rows, a.kv_heads, a.max_splits);
-  if (a.kv.f32)
-    attention_split_kernel<float><<<grid, kThreads, lds, stream>>>(a);
-  else
-    attention_split_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a);
-  attention_combine_kernel<<<dim3(a.rows, a.q_heads), 128, 0, stream>>>(a);
+  const bool mfma_path = attention_uses_mfma(a.head_dim, a.kv.f32 != 0);
+  if (mfma_path) {
+    if (a.work_count > 0) {
+      if (a.head_dim == 64) launch_mfma<64>(stream, a);
+      if (a.head_dim == 128) launch_mfma<128>(stream, a);
+      if (a.head_dim == 256) launch_mfma<256>(stream, a);
+    }
+  } else {
+    const int G = a.q_heads / a.kv_heads;
+    const size_t lds = ((size_t)G * a.head_dim + (size_t)G * kTile + 2 * G) * sizeof(float);
+    dim3 grid(a.rows, a.kv_heads, a.max_splits);
+    if (a.kv.f32)
+      attention_valu_kernel<float><<<grid, kThreads, lds, stream>>>(a);
+    else
+      attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a);
+  }
+  attention_combine_kernel<<<dim3(a.rows, a.q_heads), 128, 0, stream>>>(a, mfma_path ? 1 : 0);
 }
 
 }  // namespace hllm_rocm

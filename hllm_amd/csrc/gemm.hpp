@@ -36,5 +36,8 @@ struct GemmArgs {
 // Rows of the tile a launch with `rows_bound` rows uses (activation buffers are padded to it).
 int gemm_tile_rows(int rows_bound);
 void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus);
+// An explicit configuration of the table in gemm.hip (tuning), optionally forcing the K split.
+void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
+                        int config, int forced_ksplit);
 
 }  // namespace hllm_rocm

@@ -14,6 +14,45 @@ struct ItemMeta {
   uint32_t flags;          // HLLM_ITEM_*
 };
 
+// One attention work item: a block of query rows of one item against one split of the
+// keys [key_begin, key_end) (times every KV head: grid y).
+struct AttnWork {
+  int32_t item;
+  int32_t row0;       // packed row of the block's first query row
+  int32_t rows;       // query rows in the block
+  int32_t position0;  // position of the block's first query row
+  int32_t split;      // split index of the block's key range
+  int32_t splits;     // number of splits of the block's key range
+  int32_t key_begin;
+  int32_t key_end;
+};
+
+// Query rows per attention block: 64 query vectors (rows x query heads of one KV head),
+// at least one row.
+__host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ? 1 : 64 / group; }
+
+// Splits of a block's `keys` key positions: blocks of at most 16 query vectors (decode rows)
+// split every 1024 keys, larger blocks every 4096; splits are 32-key aligned and non-empty.
+__host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits) {
+  const int unit = vectors <= 16 ? 1024 : 4096;
+  int splits = (keys + unit - 1) / unit;
+  splits = splits < max_splits ? splits : max_splits;
+  const int per = ((keys + splits - 1) / splits + 31) & ~31;
+  return per;
+}
+__host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
+                                              int max_splits) {
+  const int qb = attn_block_rows(group);
+  int work = 0;
+  for (int r0 = 0; r0 < query_tokens; r0 += qb) {
+    const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
+    const int keys = first_position + r0 + rows;
+    const int per = attn_split_keys(keys, rows * group, max_splits);
+    work += (keys + per - 1) / per;
+  }
+  return work;
+}
+
 // Where each packed row of a pass comes from, built on the device from ItemMeta.
 struct PackOut {
   int32_t* cu_seqlens;     // [items + 1] exclusive prefix sum of query_tokens
@@ -24,16 +63,34 @@ struct PackOut {
   int32_t* sample_row;     // [items] packed row of each sampling item, in item order (compacted)
   int32_t* sample_item;    // [items]
   int32_t* sample_count;   // [1]
+  AttnWork* attn_work;     // attention work items (MFMA path), in item order
+  int32_t* row_splits;     // [rows] key splits of the row's attention block
+  int attn_group;          // query heads per KV head
+  int attn_max_splits;
 };
 
+// Paged KV pool: [layers][blocks][K, V][kv_heads][...] with keys as [block_tokens][head_dim]
+// (a position's key contiguous) and values transposed as [head_dim][block_tokens] (a
+// dimension's values over the block's positions contiguous), the operand layouts of the
+// attention MFMAs.
 struct KvView {
-  void* pool;              // [layers][blocks][2][kv_heads][block_tokens][head_dim]
+  void* pool;
   uint64_t layer_stride;   // elements per layer
   int32_t block_tokens;
   int32_t kv_heads;
   int32_t head_dim;
   int32_t f32;             // element type: 1 = F32, 0 = F16
 };
+__host__ __device__ inline uint64_t kv_key_index(const KvView& kv, int layer, uint64_t block, int offset,
+                                                 int head, int d) {
+  return (uint64_t)layer * kv.layer_stride +
+         ((block * 2 * kv.kv_heads + head) * kv.block_tokens + offset) * kv.head_dim + d;
+}
+__host__ __device__ inline uint64_t kv_value_index(const KvView& kv, int layer, uint64_t block, int offset,
+                                                   int head, int d) {
+  return (uint64_t)layer * kv.layer_stride +
+         (((block * 2 + 1) * kv.kv_heads + head) * kv.head_dim + d) * kv.block_tokens + offset;
+}
 
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
                  const int32_t* last_token, const int32_t* block_table, int table_width,
@@ -65,6 +122,9 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
 struct AttentionArgs {
   const float* q;              // [rows][Q][D]
   int rows, q_heads, kv_heads, head_dim;
+  const AttnWork* work;        // MFMA path work list and its host-computed size
+  int work_count;
+  const int32_t* row_splits;
   const int32_t* row_item;
   const int32_t* row_position;
   const ItemMeta* items;
@@ -81,6 +141,8 @@ struct AttentionArgs {
   uint64_t out_cols_padded;
 };
 void launch_attention(hipStream_t stream, const AttentionArgs& a);
+// Whether launch_attention uses the MFMA kernel (and hence the pack kernel's work list).
+bool attention_uses_mfma(int head_dim, bool kv_f32);
 
 // Row-wise first maximum over `cols` F32 values per row (greedy sampling) and a
 // non-finite flag (bit 1 of flags).

@@ -38,23 +38,29 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
                                                      const int32_t* last_token,
                                                      const int32_t* block_table, int table_width,
                                                      int block_tokens, PackOut out) {
-  __shared__ int scratch[8];
+  __shared__ int scratch[12];
   const int i = blockIdx.x;
-  int offset = 0, samples = 0;
+  int offset = 0, samples = 0, work = 0;
   for (int j = threadIdx.x; j < i; j += blockDim.x) {
     offset += (int)items[j].query_tokens;
     samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
+    if (out.attn_work)
+      work += attn_item_work((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
+                             out.attn_max_splits);
   }
   offset = wave_sum_int(offset);
   samples = wave_sum_int(samples);
+  work = wave_sum_int(work);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     scratch[wave] = offset;
     scratch[4 + wave] = samples;
+    scratch[8 + wave] = work;
   }
   __syncthreads();
   offset = scratch[0] + scratch[1] + scratch[2] + scratch[3];
   samples = scratch[4] + scratch[5] + scratch[6] + scratch[7];
+  work = scratch[8] + scratch[9] + scratch[10] + scratch[11];
   const ItemMeta it = items[i];
   const bool sample = (it.flags & HLLM_ITEM_SAMPLE) != 0;
   if (threadIdx.x == 0) {
@@ -77,6 +83,22 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     out.row_slot[r] = table[position / block_tokens] * block_tokens + position % block_tokens;
     out.row_token[r] = (it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) ? last_token[it.sequence]
                                                                  : host_tokens[r];
+  }
+  // Attention blocks of this item: query rows [r0, r0 + rows) against keys [0, first + r0 + rows).
+  if (out.attn_work && threadIdx.x == 0) {
+    const int group = out.attn_group, qb = attn_block_rows(group);
+    const int q = (int)it.query_tokens, first = (int)it.first_position;
+    for (int r0 = 0; r0 < q; r0 += qb) {
+      const int rows = min(qb, q - r0);
+      const int keys = first + r0 + rows;
+      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits);
+      const int splits = (keys + per - 1) / per;
+      for (int s = 0; s < splits; ++s) {
+        out.attn_work[work++] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per,
+                                         min(keys, (s + 1) * per)};
+      }
+      for (int r = 0; r < rows; ++r) out.row_splits[offset + r0 + r] = splits;
+    }
   }
 }
 
@@ -150,10 +172,8 @@ __device__ inline uint64_t kv_index(const KvView& kv, int layer, int slot, int w
                                     int d) {
   const int block = slot / kv.block_tokens;
   const int offset = slot - block * kv.block_tokens;
-  return (uint64_t)layer * kv.layer_stride +
-         (((uint64_t)block * 2 + which) * kv.kv_heads + head) * (uint64_t)kv.block_tokens *
-             kv.head_dim +
-         (uint64_t)offset * kv.head_dim + d;
+  return which ? kv_value_index(kv, layer, (uint64_t)block, offset, head, d)
+               : kv_key_index(kv, layer, (uint64_t)block, offset, head, d);
 }
 
 // One wave per head. Lane l holds elements d = l + 64 j. Head dimensions are powers of two

@@ -180,7 +180,9 @@ class Stage {
   // workspaces
   DeviceMemory h_, a0_hi_, a0_lo_, a1_hi_, a1_lo_, qkv_, q_, attn_partial_;
   DeviceMemory gemm_ws_, gemm_counters_, logits_, argmax_val_, argmax_idx_, tokens_, flags_;
-  DeviceMemory items_dev_, host_tokens_dev_, pack_buf_, boundary_dev_, staging_;
+  DeviceMemory items_dev_, host_tokens_dev_, pack_buf_, boundary_dev_, staging_, attn_work_;
+  bool mfma_attention_ = false;
+  uint64_t attn_work_max_ = 0;
   size_t gemm_ws_floats_ = 0;
   int gemm_counter_count_ = 0;
   PackOut pack_{};
@@ -342,7 +344,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   flags_.allocate(sizeof(int32_t), "flags");
   items_dev_.allocate(items_max_ * sizeof(ItemMeta), "items");
   host_tokens_dev_.allocate(R * sizeof(int32_t), "tokens");
-  pack_buf_.allocate(((items_max_ + 1) + 4 * R + 2 * items_max_ + 1) * sizeof(int32_t), "pack");
+  pack_buf_.allocate(((items_max_ + 1) + 5 * R + 2 * items_max_ + 1) * sizeof(int32_t), "pack");
   {
     int32_t* p = pack_buf_.as<int32_t>();
     pack_.cu_seqlens = p;
@@ -360,6 +362,19 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     pack_.sample_item = p;
     p += items_max_;
     pack_.sample_count = p;
+    p += 1;
+    pack_.row_splits = p;
+  }
+  mfma_attention_ = attention_uses_mfma((int)D_, kv_f32_);
+  if (mfma_attention_) {
+    // Upper bound of attention work items: per item, one per 64-vector block per split.
+    const uint64_t group = Q_ / K_;
+    const uint64_t qb = group >= 64 ? 1 : 64 / group;
+    attn_work_max_ = (R / qb + items_max_) * kMaxSplits;
+    attn_work_.allocate(attn_work_max_ * sizeof(AttnWork), "attention work");
+    pack_.attn_work = attn_work_.as<AttnWork>();
+    pack_.attn_group = (int)group;
+    pack_.attn_max_splits = kMaxSplits;
   }
   if (!c.first_stage || !c.final_stage) boundary_dev_.allocate(R * H_ * 2, "boundary");
   pin_items_.allocate(items_max_ * sizeof(ItemMeta));
@@ -384,6 +399,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   if (blocks_total_ == 0) fail(HLLM_RESOURCE_EXHAUSTED, "KV cache budget holds no block");
   if (blocks_total_ * bt > 0x7fffffffull) blocks_total_ = 0x7fffffffull / bt;
   kv_pool_.allocate(blocks_total_ * block_bytes_all_layers, "KV cache");
+  HIP_CHECK(hipMemsetAsync(kv_pool_.ptr, 0, kv_pool_.bytes, stream_));
   kv_.pool = kv_pool_.ptr;
   kv_.block_tokens = bt;
   kv_.kv_heads = (int)K_;
@@ -436,6 +452,8 @@ void Stage::check_sizes() {
     fail(HLLM_INCOMPATIBLE_WORKER, "model dimensions exceed this worker's limits");
   if (c.kv_block_tokens && (c.kv_block_tokens & (c.kv_block_tokens - 1)))
     fail(HLLM_INVALID_REQUEST, "KV block tokens must be a power of two");
+  if (c.kv_block_tokens && c.kv_block_tokens < 32 && c.execution_dtype == HLLM_DTYPE_F16)
+    fail(HLLM_INVALID_REQUEST, "KV blocks of an F16 stage hold at least 32 tokens");
   if (c.max_pass_rows > (1u << 16)) fail(HLLM_INVALID_REQUEST, "max pass rows too large");
 }
 
@@ -678,7 +696,9 @@ void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values)
       for (uint64_t which = 0; which < 2; ++which)
         for (uint64_t hd = 0; hd < K_; ++hd)
           for (uint64_t d = 0; d < D_; ++d) {
-            const uint64_t i = ((which * K_ + hd) * bt + (p - p0)) * D_ + d;
+            // keys [head][position][dim], values transposed [head][dim][position]
+            const uint64_t i = which ? ((K_ + hd) * D_ + d) * bt + (p - p0)
+                                     : (hd * bt + (p - p0)) * D_ + d;
             float v;
             if (kv_f32_) {
               std::memcpy(&v, block.data() + i * 4, 4);
@@ -864,6 +884,13 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     std::memcpy(pin_boundary_.ptr, pass.boundary_in, count * 2);
   }
   if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+  int attn_work_count = 0;
+  if (mfma_attention_) {
+    for (uint32_t i = 0; i < n; ++i)
+      attn_work_count += attn_item_work((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
+                                        (int)(Q_ / K_), kMaxSplits);
+    if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
+  }
 
   // ---- device work
   try {
@@ -914,6 +941,9 @@ void Stage::submit(const hllm_rocm_pass& pass) {
                                q_.as<float>());
       });
       AttentionArgs at{};
+      at.work = attn_work_.as<AttnWork>();
+      at.work_count = attn_work_count;
+      at.row_splits = pack_.row_splits;
       at.q = q_.as<float>();
       at.rows = R;
       at.q_heads = (int)Q_;
