@@ -89,18 +89,41 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   float m = -INFINITY, l = 0.0f;
 
   const int stride = split_keys ? 4 : 1;
-  for (int t = w.key_begin + 32 * (split_keys ? wave : 0); t < w.key_end; t += 32 * stride) {
+  // K and V fragments of one 32-key tile; the next tile's are loaded while this one is used.
+  struct Tile {
+    half8 k0[KK], k1[KK];
+    half8 v[DF];
+  };
+  auto fetch = [&](int t, Tile& f) {
     const int logical = t / bt;
     const uint64_t blk = (uint64_t)table[logical];
     const int off = t - logical * bt;
     const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
+    const _Float16* vb = pool + (((blk * 2 + 1) * KVH + kvh) * D) * bt + off;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      f.k0[kk] = *reinterpret_cast<const half8*>(kb + (size_t)col * D + 32 * kk + 8 * quad);
+      f.k1[kk] = *reinterpret_cast<const half8*>(kb + (size_t)(16 + col) * D + 32 * kk + 8 * quad);
+    }
+#pragma unroll
+    for (int df = 0; df < DF; ++df) {
+      const _Float16* vrow = vb + (size_t)(16 * df + col) * bt;
+      const half4 a0 = *reinterpret_cast<const half4*>(vrow + 4 * quad);
+      const half4 a1 = *reinterpret_cast<const half4*>(vrow + 16 + 4 * quad);
+      f.v[df] = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    }
+  };
+  int t = w.key_begin + 32 * (split_keys ? wave : 0);
+  Tile cur, nxt;
+  if (t < w.key_end) fetch(t, cur);
+  for (; t < w.key_end; t += 32 * stride) {
+    const int tn = t + 32 * stride;
+    if (tn < w.key_end) fetch(tn, nxt);
     floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      const half8 k0 = *reinterpret_cast<const half8*>(kb + (size_t)col * D + 32 * kk + 8 * quad);
-      const half8 k1 = *reinterpret_cast<const half8*>(kb + (size_t)(16 + col) * D + 32 * kk + 8 * quad);
-      s0 = mfma(k0, qf[kk], s0);
-      s1 = mfma(k1, qf[kk], s1);
+      s0 = mfma(cur.k0[kk], qf[kk], s0);
+      s1 = mfma(cur.k1[kk], qf[kk], s1);
     }
     float sc[8];
 #pragma unroll
@@ -129,7 +152,6 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
     psum += __shfl_xor(psum, 32, 64);
     l = l * alpha + psum;
     m = m_new;
-    const _Float16* vb = pool + (((blk * 2 + 1) * KVH + kvh) * D) * bt + off;
     // A tile that runs past the key range reads cache slots no pass has written: zero
     // them, since a zero probability does not cancel a non-finite value.
     const bool tail = t + 32 > w.key_end;
@@ -139,10 +161,7 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       o[df][1] *= alpha;
       o[df][2] *= alpha;
       o[df][3] *= alpha;
-      const _Float16* vrow = vb + (size_t)(16 * df + col) * bt;
-      const half4 a0 = *reinterpret_cast<const half4*>(vrow + 4 * quad);
-      const half4 a1 = *reinterpret_cast<const half4*>(vrow + 16 + 4 * quad);
-      half8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      half8 av = cur.v[df];
       if (tail) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -152,6 +171,7 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       }
       o[df] = mfma(av, pf, o[df]);
     }
+    cur = nxt;
   }
 
   float m_fin = m, l_fin = l;

@@ -156,33 +156,14 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   }
 
   if (a.ksplit > 1) {
-    float* ws = a.workspace + (size_t)tile * a.ksplit * BM * BN;
+    // Partial tile of this K split; gemm_reduce_kernel sums the splits in order and applies
+    // the epilogue after this kernel completes (no device-scope fences needed).
+    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
     for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
       const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-      *reinterpret_cast<floatx4*>(ws + (size_t)split * BM * BN + m * BN + n) =
-          *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
+      *reinterpret_cast<floatx4*>(ws + m * BN + n) = *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
     }
-    __threadfence();
-    __syncthreads();
-    int* last = reinterpret_cast<int*>(lds + (size_t)BM * LDT);
-    if (threadIdx.x == 0) *last = atomicAdd(a.counters + tile, 1) == a.ksplit - 1;
-    __syncthreads();
-    if (!*last) return;
-    __threadfence();
-    for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
-      const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-      floatx4 s = *reinterpret_cast<const floatx4*>(ws + m * BN + n);
-      for (int p = 1; p < a.ksplit; ++p) {
-        const floatx4 t = *reinterpret_cast<const floatx4*>(ws + (size_t)p * BM * BN + m * BN + n);
-        s[0] += t[0];
-        s[1] += t[1];
-        s[2] += t[2];
-        s[3] += t[3];
-      }
-      *reinterpret_cast<floatx4*>(lds + m * LDT + n) = s;
-    }
-    if (threadIdx.x == 0) a.counters[tile] = 0;
-    __syncthreads();
+    return;
   }
 
   // Epilogue from the LDS tile.
@@ -232,6 +213,256 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   }
 }
 
+// Activation-staged variant: the workgroup's four waves split N (each owns NFW weight
+// fragment rows), the activation fragments of the tile are staged once per workgroup in LDS
+// (chunks of KC k-steps, double-buffered), and every wave streams its own weight fragments
+// through a ring of P k-steps. Activation traffic per weight byte drops to BM / BN.
+template <int MF, int NFW, int KC, int P, int PREC>
+__global__ void __launch_bounds__(256)
+    gemm_xlds_kernel(GemmArgs a, int n_tiles, int tiles) {
+  constexpr int BM = 16 * MF, BN = 64 * NFW, NT = 256, LDT = BN + 4;
+  constexpr bool kLoA = PREC >= kSplitA, kLoB = PREC == kSplitAB;
+  constexpr int XP = kLoA ? 2 : 1;                  // activation parts (hi, lo)
+  constexpr int CHUNK = MF * KC * 64 * XP;          // half8s per staged chunk
+  extern __shared__ float lds[];
+  half8* xs = reinterpret_cast<half8*>(lds);        // [2][XP][MF][KC][64]
+  const int M = a.device_m ? *a.device_m : a.M;
+  const int split = blockIdx.x / tiles;
+  const int tile = blockIdx.x - split * tiles;
+  const int tile_n = tile % n_tiles, tile_m = tile / n_tiles;
+  if (tile_m * BM >= M) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int KT = (int)(a.Kp >> 5);
+  const int per = ((KT + a.ksplit - 1) / a.ksplit + KC - 1) / KC * KC;
+  const int kt0 = split * per, kt1 = min(KT, kt0 + per);
+  const int nfrag0 = tile_n * (BN / 16) + wave * NFW;
+  const int mfrag0 = tile_m * MF;
+  const size_t frag_stride = (size_t)KT * 64;
+  const half8* W = reinterpret_cast<const half8*>(a.w_hi) + (size_t)nfrag0 * frag_stride + lane;
+  const half8* WL = reinterpret_cast<const half8*>(a.w_lo) + (size_t)nfrag0 * frag_stride + lane;
+  const half8* X = reinterpret_cast<const half8*>(a.x_hi) + (size_t)mfrag0 * frag_stride;
+  const half8* XL = reinterpret_cast<const half8*>(a.x_lo) + (size_t)mfrag0 * frag_stride;
+
+  floatx4 acc[MF][NFW], acc2[MF][NFW];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int j = 0; j < NFW; ++j) {
+      acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      acc2[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  const int steps = kt1 > kt0 ? kt1 - kt0 : 0;
+  const int chunks = (steps + KC - 1) / KC;
+
+  // Staging of chunk c (k-steps kt0 + c*KC ...) into buffer c % 2: thread-strided pieces.
+  constexpr int PIECES = CHUNK / NT > 0 ? (CHUNK + NT - 1) / NT : 1;
+  half8 stage[PIECES];
+  auto fetch_x = [&](int c) {
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int e = threadIdx.x + q * NT;  // (part, i, j, lane) flattened
+      if (e < CHUNK) {
+        const int ln = e & 63, j = (e >> 6) % KC, i = (e / (64 * KC)) % MF, part = e / (64 * KC * MF);
+        const int kt = kt0 + c * KC + j;
+        const half8* src = part ? XL : X;
+        stage[q] = kt < kt1 ? src[(size_t)i * frag_stride + (size_t)kt * 64 + ln] : half8{};
+      }
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int e = threadIdx.x + q * NT;
+      if (e < CHUNK) xs[buf * CHUNK + e] = stage[q];
+    }
+  };
+
+  half8 rb[P][NFW];
+  half8 rbl[kLoB ? P : 1][kLoB ? NFW : 1];
+  auto load_w = [&](int slot, int kt) {
+#pragma unroll
+    for (int j = 0; j < NFW; ++j) rb[slot][j] = W[j * frag_stride + (size_t)kt * 64];
+    if constexpr (kLoB) {
+#pragma unroll
+      for (int j = 0; j < NFW; ++j) rbl[slot][j] = WL[j * frag_stride + (size_t)kt * 64];
+    }
+  };
+#pragma unroll
+  for (int sl = 0; sl < P; ++sl)
+    if (sl < steps) load_w(sl, kt0 + sl);
+  if (chunks > 0) {
+    fetch_x(0);
+    store_x(0);
+  }
+  __syncthreads();
+  for (int c = 0; c < chunks; ++c) {
+    if (c + 1 < chunks) fetch_x(c + 1);
+    const half8* xb = xs + (c & 1) * CHUNK;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int step = c * KC + j;
+      if (step < steps) {
+        const int slot = j % P;  // P divides KC, so step % P == j % P (a register index)
+        half8 x[MF];
+#pragma unroll
+        for (int i = 0; i < MF; ++i) x[i] = xb[(i * KC + j) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+          for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[slot][n], x[i], acc[i][n]);
+        if constexpr (kLoA) {
+#pragma unroll
+          for (int i = 0; i < MF; ++i) {
+            const half8 xl = xb[MF * KC * 64 + (i * KC + j) * 64 + lane];
+#pragma unroll
+            for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rb[slot][n], xl, acc2[i][n]);
+          }
+        }
+        if constexpr (kLoB) {
+#pragma unroll
+          for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rbl[slot][n], x[i], acc2[i][n]);
+        }
+        if (step + P < steps) load_w(slot, kt0 + step + P);
+      }
+    }
+    if (c + 1 < chunks) store_x((c + 1) & 1);
+    __syncthreads();
+  }
+
+  // Output tile in LDS (reusing the staging area): each wave owns its columns.
+  float* tile_out = lds;
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int n = 0; n < NFW; ++n) {
+      floatx4 v = acc[i][n];
+      if constexpr (kLoA) {
+        v[0] += acc2[i][n][0] * kLoUnscale;
+        v[1] += acc2[i][n][1] * kLoUnscale;
+        v[2] += acc2[i][n][2] * kLoUnscale;
+        v[3] += acc2[i][n][3] * kLoUnscale;
+      }
+      const int m = i * 16 + (lane & 15);
+      const int col = (wave * NFW + n) * 16 + (lane >> 4) * 4;
+      *reinterpret_cast<floatx4*>(tile_out + m * LDT + col) = v;
+    }
+  __syncthreads();
+  if (a.ksplit > 1) {
+    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
+    for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
+      const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
+      *reinterpret_cast<floatx4*>(ws + m * BN + n) = *reinterpret_cast<const floatx4*>(tile_out + m * LDT + n);
+    }
+    return;
+  }
+  const int m_base = tile_m * BM, n_base = tile_n * BN;
+  if (a.epilogue == kEpiSwiglu) {
+    constexpr int GROUPS = BN / 64;
+    for (int e = threadIdx.x; e < BM * GROUPS * 4; e += NT) {
+      const int m = e / (GROUPS * 4), g = (e / 4) % GROUPS, c8 = e % 4;
+      const uint64_t col = (uint64_t)(n_base / 64 + g) * 32 + c8 * 8;
+      if (m_base + m >= M || col >= a.out_cols_padded) continue;
+      half8 vh, vl;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float y = silu_mul(tile_out[m * LDT + g * 64 + c8 * 8 + t], tile_out[m * LDT + g * 64 + 32 + c8 * 8 + t]);
+        vh[t] = to_half(y);
+        vl[t] = to_half((y - (float)vh[t]) * kLoScale);
+      }
+      const uint64_t at = flayout_index(m_base + m, col, a.out_cols_padded);
+      *reinterpret_cast<half8*>(a.out_hi + at) = vh;
+      if (a.out_lo) *reinterpret_cast<half8*>(a.out_lo + at) = vl;
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < BM * (BN / 4); e += NT) {
+    const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
+    const int gm = m_base + m;
+    if (gm >= M) continue;
+    float* out = a.out + (size_t)gm * a.ldo + n_base + n;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (n_base + n + t < a.N) {
+        const float v = tile_out[m * LDT + n + t];
+        if (a.epilogue == kEpiResidual)
+          out[t] += v;
+        else
+          out[t] = v;
+      }
+    }
+  }
+}
+
+// Sum of a tile's K-split partials (in split order) plus the epilogue. One thread per 8
+// consecutive outputs of one row (8 activations for SwiGLU).
+template <int BM, int BN>
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a, int n_tiles, int tiles) {
+  const int M = a.device_m ? *a.device_m : a.M;
+  const int per_tile = BM * BN / 8;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)tiles * per_tile) return;
+  const int tile = (int)(e / per_tile);
+  const int rem = (int)(e - (int64_t)tile * per_tile);
+  const int tile_n = tile % n_tiles, tile_m = tile / n_tiles;
+  const float* ws = a.workspace + (size_t)tile * a.ksplit * BM * BN;
+  if (a.epilogue == kEpiSwiglu) {
+    // rem -> (row m, 64-column group g, 8-wide chunk c8 of the 32 activations of the group)
+    constexpr int GROUPS = BN / 64;
+    const int m = rem / (GROUPS * 4), g = (rem / 4) % GROUPS, c8 = rem % 4;
+    if (rem >= BM * GROUPS * 4) return;
+    const uint64_t col = (uint64_t)(tile_n * (BN / 64) + g) * 32 + c8 * 8;
+    if (tile_m * BM + m >= M || col >= a.out_cols_padded) return;
+    float gate[8], up[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) gate[t] = up[t] = 0.0f;
+    for (int p = 0; p < a.ksplit; ++p) {
+      const float* src = ws + (size_t)p * BM * BN + m * BN + g * 64 + c8 * 8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        gate[t] += src[t];
+        up[t] += src[32 + t];
+      }
+    }
+    half8 vh, vl;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float y = silu_mul(gate[t], up[t]);
+      vh[t] = to_half(y);
+      vl[t] = to_half((y - (float)vh[t]) * kLoScale);
+    }
+    const uint64_t at = flayout_index(tile_m * BM + m, col, a.out_cols_padded);
+    *reinterpret_cast<half8*>(a.out_hi + at) = vh;
+    if (a.out_lo) *reinterpret_cast<half8*>(a.out_lo + at) = vl;
+    return;
+  }
+  const int m = rem / (BN / 8), n = (rem % (BN / 8)) * 8;
+  const int gm = tile_m * BM + m, gn = tile_n * BN + n;
+  if (gm >= M) return;
+  float v[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) v[t] = 0.0f;
+#pragma unroll 4
+  for (int p = 0; p < a.ksplit; ++p) {
+    const float* src = ws + (size_t)p * BM * BN + m * BN + n;
+    const floatx4 x0 = *reinterpret_cast<const floatx4*>(src);
+    const floatx4 x1 = *reinterpret_cast<const floatx4*>(src + 4);
+    v[0] += x0[0]; v[1] += x0[1]; v[2] += x0[2]; v[3] += x0[3];
+    v[4] += x1[0]; v[5] += x1[1]; v[6] += x1[2]; v[7] += x1[3];
+  }
+  float* out = a.out + (size_t)gm * a.ldo + gn;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (gn + t < a.N) {
+      if (a.epilogue == kEpiResidual)
+        out[t] += v[t];
+      else
+        out[t] = v[t];
+    }
+  }
+}
+
 template <int MF, int NF, int WM, int WN, int WK, int P, int PREC>
 void run(dim3 grid, int threads, size_t lds, hipStream_t stream, const GemmArgs& a, int n_tiles,
          int tiles, int tiles_padded) {
@@ -254,6 +485,7 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
   const int KT = (int)(a.Kp >> 5);
+  if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
   const int tiles = n_tiles * m_tiles;
   int ksplit = 1;
   if (forced_ksplit > 0) {
@@ -263,8 +495,7 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
   }
   ksplit = std::min(ksplit, std::max(1, KT / (WK * min_k_per_wave)));
   const int tiles_padded = (tiles + kXcds - 1) / kXcds * kXcds;
-  if ((size_t)tiles_padded * ksplit * BM * BN > a.workspace_floats || tiles_padded > a.counter_count)
-    ksplit = 1;
+  if ((size_t)tiles * ksplit * BM * BN > a.workspace_floats) ksplit = 1;
   a.ksplit = ksplit;
   const size_t lds = ((size_t)BM * (BN + 4) + 4) * sizeof(float);
   dim3 grid(tiles_padded * ksplit, 1, 1);
@@ -278,6 +509,46 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
     default:
       run<MF, NF, WM, WN, WK, P, kSplitAB>(grid, NT, lds, stream, a, n_tiles, tiles, tiles_padded);
       break;
+  }
+  if (ksplit > 1) {
+    const int64_t threads = (int64_t)tiles * BM * BN / 8;
+    gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles);
+  }
+}
+
+template <int MF, int NFW, int KC, int P>
+void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
+                 int forced_ksplit) {
+  constexpr int BM = 16 * MF, BN = 64 * NFW;
+  const int n_tiles = (a.N + BN - 1) / BN;
+  const int m_tiles = (rows_bound + BM - 1) / BM;
+  const int tiles = n_tiles * m_tiles;
+  const int KT = (int)(a.Kp >> 5);
+  if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
+  int ksplit = forced_ksplit > 0 ? forced_ksplit : (tiles < target_ctas ? (target_ctas + tiles - 1) / tiles : 1);
+  ksplit = std::min(ksplit, std::max(1, KT / (2 * KC)));
+  if ((size_t)tiles * ksplit * BM * BN > a.workspace_floats) ksplit = 1;
+  a.ksplit = ksplit;
+  const int xp = prec >= kSplitA ? 2 : 1;
+  const size_t lds = std::max((size_t)2 * MF * KC * 64 * xp * 16, (size_t)BM * (BN + 4) * sizeof(float));
+  dim3 grid(tiles * ksplit);
+  auto go = [&](auto kernel) {
+    static bool configured = false;
+    if (!configured) {
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024));
+      configured = true;
+    }
+    kernel<<<grid, 256, lds, stream>>>(a, n_tiles, tiles);
+  };
+  switch (prec) {
+    case kF16: go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>); break;
+    case kSplitA: go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitA>); break;
+    default: go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>); break;
+  }
+  if (ksplit > 1) {
+    const int64_t threads = (int64_t)tiles * BM * BN / 8;
+    gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles);
   }
 }
 
@@ -293,13 +564,13 @@ void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int 
                         int config, int forced_ksplit) {
   switch (config) {
     case 0:
-      launch_config<1, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      launch_config<1, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 1:
-      launch_config<2, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      launch_config<2, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 2:
-      launch_config<4, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      launch_config<4, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 4:
       launch_config<1, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
@@ -309,6 +580,24 @@ void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int 
       break;
     case 6:
       launch_config<4, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      break;
+    case 7:  // activation-staged: BM 16 x BN 128
+      launch_xlds<1, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+      break;
+    case 8:  // BM 32 x BN 128
+      launch_xlds<2, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+      break;
+    case 9:  // BM 64 x BN 128
+      launch_xlds<4, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+      break;
+    case 10:  // BM 64 x BN 256
+      launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+      break;
+    case 11:  // BM 128 x BN 128
+      launch_xlds<8, 2, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+      break;
+    case 12:  // BM 128 x BN 64
+      launch_xlds<8, 1, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
       break;
     default:
       launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
@@ -331,9 +620,7 @@ void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bo
   }();
   int config = gemm_default_config(rows_bound);
   if (forced >= 0 && (rows_bound <= 64) == (forced != 3)) config = forced;
-  // Splitting K across workgroups needs device-scope fences around the partial tiles, which
-  // cost more than the parallelism gains (measured); one workgroup per tile by default.
-  launch_gemm_config(stream, args, prec, rows_bound, cus, config, 1);
+  launch_gemm_config(stream, args, prec, rows_bound, cus, config, 0);
 }
 
 }  // namespace hllm_rocm

@@ -19,6 +19,7 @@ struct GemmArgs {
   int M;                       // rows, unless device_m is set
   const int32_t* device_m;     // rows read on the device (sampled rows), <= the launch bound
   int N;                       // output features
+  uint64_t w_rows_padded;      // weight rows allocated (tiles never read past them)
   uint64_t Kp;                 // K padded to 32 (same for both operands)
   int ksplit;                  // set by the launcher
   float* workspace;            // split-K partial tiles

@@ -31,10 +31,11 @@ struct AttnWork {
 // at least one row.
 __host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ? 1 : 64 / group; }
 
-// Splits of a block's `keys` key positions: blocks of at most 16 query vectors (decode rows)
-// split every 1024 keys, larger blocks every 4096; splits are 32-key aligned and non-empty.
+// Splits of a block's `keys` key positions, every 1024 keys (shorter serial chains per
+// workgroup); splits are 32-key aligned and non-empty.
 __host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits) {
-  const int unit = vectors <= 16 ? 1024 : 4096;
+  (void)vectors;
+  const int unit = 1024;
   int splits = (keys + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = ((keys + splits - 1) / splits + 31) & ~31;

@@ -138,6 +138,9 @@ __global__ void boundary_encode_kernel(const float* h, uint64_t n, uint16_t* out
 
 // ------------------------------------------------------------------ RMSNorm -> operand
 
+// One block per row; each thread keeps its 8-column chunks in registers between the
+// square sum and the scaled store (hidden sizes up to 256 * 8 * kNormChunks).
+constexpr int kNormChunks = 4;
 __global__ void __launch_bounds__(kBlock) rmsnorm_flayout_kernel(
     const float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
     const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
@@ -147,16 +150,35 @@ __global__ void __launch_bounds__(kBlock) rmsnorm_flayout_kernel(
   if (r >= count) return;
   const int src = row_index ? row_index[r] : r;
   const float* x = h + (size_t)src * hidden;
+  float v[kNormChunks][8];
   float squares = 0.0f;
-  for (int c = threadIdx.x; c < hidden; c += blockDim.x) squares += x[c] * x[c];
+  const bool vec = (hidden & 7) == 0;
+#pragma unroll
+  for (int q = 0; q < kNormChunks; ++q) {
+    const int c0 = (threadIdx.x + q * blockDim.x) * 8;
+    if (vec && c0 < hidden) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(x + c0);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(x + c0 + 4);
+      v[q][0] = a[0]; v[q][1] = a[1]; v[q][2] = a[2]; v[q][3] = a[3];
+      v[q][4] = b[0]; v[q][5] = b[1]; v[q][6] = b[2]; v[q][7] = b[3];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[q][j] = c0 + j < hidden ? x[c0 + j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) squares += v[q][j] * v[q][j];
+  }
   squares = block_sum(squares, scratch);
   const float inverse = 1.0f / sqrtf(squares / (float)hidden + eps);
-  for (int c0 = threadIdx.x * 8; c0 < (int)cols_padded; c0 += blockDim.x * 8) {
+#pragma unroll
+  for (int q = 0; q < kNormChunks; ++q) {
+    const int c0 = (threadIdx.x + q * blockDim.x) * 8;
+    if (c0 >= (int)cols_padded) continue;
     half8 vh, vl;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int c = c0 + j;
-      const float y = c < hidden ? (x[c] * inverse) * weight[c] : 0.0f;
+      const float y = c < hidden ? (v[q][j] * inverse) * weight[c] : 0.0f;
       vh[j] = to_half(y);
       vl[j] = to_half((y - (float)vh[j]) * kLoScale);
     }
@@ -186,6 +208,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   const int r = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
   const int heads = q_heads + 2 * kv_heads;
+  const int head_first = blockIdx.y * waves + wave;  // one head per wave
   const int D = head_dim, half = D / 2;
   const int per_lane = D >= 64 ? D / 64 : 1;
   const int position = row_position[r];
@@ -193,7 +216,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   const float* row = qkv + (size_t)r * heads * D;
   const float* cos_row = rope_cos + (size_t)position * half;
   const float* sin_row = rope_sin + (size_t)position * half;
-  for (int head = wave; head < heads; head += waves) {
+  for (int head = head_first; head < heads; head += waves * gridDim.y) {
     const bool is_q = head < q_heads;
     const bool is_v = head >= q_heads + kv_heads;
     const float* src = row + head * D;
@@ -464,7 +487,8 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
                             int head_dim, const float* q_norm, const float* k_norm, float eps,
                             const float* rope_cos, const float* rope_sin, const int32_t* row_position,
                             const int32_t* row_slot, KvView kv, int layer, float* q_out) {
-  qkv_rope_append_kernel<<<rows, kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
+  const int heads = q_heads + 2 * kv_heads;
+  qkv_rope_append_kernel<<<dim3(rows, (heads + 3) / 4), kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
                                                       k_norm, eps, rope_cos, rope_sin, row_position,
                                                       row_slot, kv, layer, q_out);
 }

@@ -236,7 +236,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   // ---- weights
   const size_t wel = w_f32_ ? 2 : 1;  // hi (+ lo) parts
   auto matrix = [&](Matrix& m, uint64_t rows, uint64_t cols, const char* what) {
-    m.rows_padded = pad_to(rows, 128);
+    m.rows_padded = pad_to(rows, 256);  // whole GEMM weight tiles (at most 256 features)
     m.cols_padded = pad32(cols);
     const size_t bytes = m.rows_padded * m.cols_padded * 2;
     m.hi.allocate(bytes, what);
@@ -448,7 +448,7 @@ void Stage::check_sizes() {
       !(c.weight_dtype == HLLM_DTYPE_F32 && c.execution_dtype == HLLM_DTYPE_F32))
     fail(HLLM_INCOMPATIBLE_WORKER, "unsupported resident/execution precision contract");
   if (c.maximum_sequence_length > (1u << 24) || c.vocabulary_size > 0x7fffffffull ||
-      c.hidden_size > (1u << 16) || c.intermediate_size > (1u << 18))
+      c.hidden_size > 8192 || c.intermediate_size > (1u << 18))
     fail(HLLM_INCOMPATIBLE_WORKER, "model dimensions exceed this worker's limits");
   if (c.kv_block_tokens && (c.kv_block_tokens & (c.kv_block_tokens - 1)))
     fail(HLLM_INVALID_REQUEST, "KV block tokens must be a power of two");
@@ -795,6 +795,7 @@ void Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, cons
   a.x_lo = x_lo;
   a.M = rows;
   a.N = n;
+  a.w_rows_padded = w.rows_padded;
   a.Kp = w.cols_padded;
   a.workspace = gemm_ws_.as<float>();
   a.workspace_floats = gemm_ws_floats_;
