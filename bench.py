@@ -297,6 +297,9 @@ def main():
     ap.add_argument("--layers", type=int, default=0, help="truncate the model (debug only)")
     ap.add_argument("--decode-steps", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-gb", type=float, default=48.0, help="paged KV pool size (GiB)")
+    ap.add_argument("--kv-block", type=int, default=0, help="tokens per KV block (0 = default)")
+    ap.add_argument("--decode-only", action="store_true", help="only the pure-decode measurement")
     ap.add_argument("--skip-extras", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -308,7 +311,8 @@ def main():
     if args.layers:
         shape = synthetic.with_layers(shape, args.layers)
     rows_max = args.chunk + args.concurrency
-    cfg = model.stage_config(shape, execution="f16", kv_cache_bytes=48 << 30,
+    cfg = model.stage_config(shape, execution="f16", kv_cache_bytes=int(args.kv_gb * (1 << 30)),
+                             kv_block_tokens=args.kv_block,
                              max_sequences=4 * args.concurrency,
                              max_pass_rows=((rows_max + 127) // 128) * 128, max_seq=4096)
     t0 = time.perf_counter()
@@ -318,6 +322,11 @@ def main():
         f"{stage.weight_memory().device_bytes / 1e9:.2f} GB")
 
     rng = np.random.default_rng(args.seed)
+    if args.decode_only:
+        d = decode_bench(stage, shape, rng, args.concurrency, args.decode_steps)
+        print(json.dumps({"decode": d}), flush=True)
+        stage.close()
+        return
     engine = Engine(stage, args.concurrency, args.chunk,
                     request_stream(np.random.default_rng(args.seed + 1), shape.vocab, args.rate))
     for i in range(args.warmup):

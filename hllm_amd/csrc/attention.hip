@@ -6,8 +6,9 @@
 // (v_mfma_f32_16x16x32_f16 with a cached key fragment as the A operand, loaded straight
 // from the paged cache), so that each lane holds four positions of one query vector; the
 // probabilities of 32 positions then form the B operand of O^T = V^T P directly in
-// registers: both operands list the positions in the same k-slot order (the values are
-// stored transposed per block, so V^T rows load as 8-byte pieces). Online softmax runs in
+// registers: both operands list the positions in the same k-slot order (key rows are loaded
+// permuted so a lane's scores are 8 consecutive positions, and the values are stored
+// transposed per block, so each V^T row segment is one 16-byte load). Online softmax runs in
 // F32 per query vector. Blocks of at most 16 vectors (decode rows) let the four waves
 // interleave 32-key tiles and merge through LDS; larger blocks give each wave 16 vectors.
 //
@@ -67,10 +68,22 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   const bool v_ok = v < nvec;
   const int vr = v / G, vg = v - vr * G;
   const int my_pos = w.position0 + vr;
-  if (!split_keys && vf * 16 >= nvec) return;  // no __syncthreads on this path
   const int seq = a.items[w.item].sequence;
-  const int32_t* table = a.block_table + (size_t)seq * a.table_width;
   const int bt = a.kv.block_tokens, KVH = a.kv_heads;
+  if (!split_keys && vf * 16 >= nvec) return;  // no __syncthreads on this path
+  // Physical blocks of the split: lane i holds the table entry of logical block chunk + i,
+  // refreshed every 64 blocks, so a tile's block is a lane read rather than a dependent
+  // global load. Tiles are 32-key aligned and blocks a multiple of 32 keys, so a tile lies
+  // in one block.
+  const int32_t* table = a.block_table + (size_t)seq * a.table_width;
+  int chunk = -64, chunk_entry = 0;
+  auto block_of = [&](int logical) -> uint64_t {
+    if (logical - chunk >= 64) {  // wave-uniform: tiles only move forward
+      chunk = logical;
+      chunk_entry = chunk + lane < a.table_width ? table[chunk + lane] : 0;
+    }
+    return (uint64_t)(uint32_t)__shfl(chunk_entry, logical - chunk, 64);
+  };
   const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
 
   // Q^T as the B operand (1/sqrt(D) folded in): lane holds Q[v][32 kk + 8 quad + j].
@@ -78,10 +91,15 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   {
     const float* qrow = a.q + ((size_t)(w.row0 + (v_ok ? vr : 0)) * a.q_heads + kvh * G + vg) * D;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
+    for (int kk = 0; kk < KK; ++kk) {
+      const floatx4 x0 = *reinterpret_cast<const floatx4*>(qrow + 32 * kk + 8 * quad);
+      const floatx4 x1 = *reinterpret_cast<const floatx4*>(qrow + 32 * kk + 8 * quad + 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        qf[kk][j] = v_ok ? to_half(qrow[32 * kk + 8 * quad + j] * a.scale) : (_Float16)0.0f;
+      for (int j = 0; j < 4; ++j) {
+        qf[kk][j] = v_ok ? to_half(x0[j] * a.scale) : (_Float16)0.0f;
+        qf[kk][4 + j] = v_ok ? to_half(x1[j] * a.scale) : (_Float16)0.0f;
+      }
+    }
   }
   floatx4 o[DF];
 #pragma unroll
@@ -96,21 +114,22 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   };
   auto fetch = [&](int t, Tile& f) {
     const int logical = t / bt;
-    const uint64_t blk = (uint64_t)table[logical];
+    const uint64_t blk = block_of(logical);
     const int off = t - logical * bt;
     const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
-    const _Float16* vb = pool + (((blk * 2 + 1) * KVH + kvh) * D) * bt + off;
+    const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
+    // Key rows are permuted so that score fragment 0 row 4q+i is position 8q+i and fragment
+    // 1 row 4q+i is position 8q+4+i: lane (q, v) then holds the scores of the 8 consecutive
+    // positions 8q..8q+7, which is also the order of its 16-byte V^T load.
+    const int r0 = 8 * (col >> 2) + (col & 3);
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      f.k0[kk] = *reinterpret_cast<const half8*>(kb + (size_t)col * D + 32 * kk + 8 * quad);
-      f.k1[kk] = *reinterpret_cast<const half8*>(kb + (size_t)(16 + col) * D + 32 * kk + 8 * quad);
+      f.k0[kk] = *reinterpret_cast<const half8*>(kb + (size_t)r0 * D + 32 * kk + 8 * quad);
+      f.k1[kk] = *reinterpret_cast<const half8*>(kb + (size_t)(r0 + 4) * D + 32 * kk + 8 * quad);
     }
 #pragma unroll
     for (int df = 0; df < DF; ++df) {
-      const _Float16* vrow = vb + (size_t)(16 * df + col) * bt;
-      const half4 a0 = *reinterpret_cast<const half4*>(vrow + 4 * quad);
-      const half4 a1 = *reinterpret_cast<const half4*>(vrow + 16 + 4 * quad);
-      f.v[df] = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      f.v[df] = *reinterpret_cast<const half8*>(vb + (size_t)(16 * df + col) * 32 + 8 * quad);
     }
   };
   int t = w.key_begin + 32 * (split_keys ? wave : 0);
@@ -128,7 +147,7 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
     float sc[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int p0 = t + 4 * quad + i, p1 = t + 16 + 4 * quad + i;
+      const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
       sc[i] = (v_ok && p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
       sc[4 + i] = (v_ok && p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
     }
@@ -164,10 +183,8 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       half8 av = cur.v[df];
       if (tail) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (t + 4 * quad + i >= w.key_end) av[i] = (_Float16)0.0f;
-          if (t + 16 + 4 * quad + i >= w.key_end) av[4 + i] = (_Float16)0.0f;
-        }
+        for (int j = 0; j < 8; ++j)
+          if (t + 8 * quad + j >= w.key_end) av[j] = (_Float16)0.0f;
       }
       o[df] = mfma(av, pf, o[df]);
     }

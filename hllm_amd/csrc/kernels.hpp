@@ -71,9 +71,10 @@ struct PackOut {
 };
 
 // Paged KV pool: [layers][blocks][K, V][kv_heads][...] with keys as [block_tokens][head_dim]
-// (a position's key contiguous) and values transposed as [head_dim][block_tokens] (a
-// dimension's values over the block's positions contiguous), the operand layouts of the
-// attention MFMAs.
+// (a position's key contiguous) and values transposed in 32-position sub-tiles as
+// [block_tokens / 32][head_dim][32] (a dimension's values over 32 positions contiguous, and
+// one 32-key attention tile's values one contiguous region): the operand layouts of the
+// attention MFMAs. Blocks hold a multiple of 32 tokens.
 struct KvView {
   void* pool;
   uint64_t layer_stride;   // elements per layer
@@ -90,7 +91,8 @@ __host__ __device__ inline uint64_t kv_key_index(const KvView& kv, int layer, ui
 __host__ __device__ inline uint64_t kv_value_index(const KvView& kv, int layer, uint64_t block, int offset,
                                                    int head, int d) {
   return (uint64_t)layer * kv.layer_stride +
-         (((block * 2 + 1) * kv.kv_heads + head) * kv.head_dim + d) * kv.block_tokens + offset;
+         ((block * 2 + 1) * kv.kv_heads + head) * (uint64_t)kv.block_tokens * kv.head_dim +
+         ((uint64_t)(offset >> 5) * kv.head_dim + d) * 32 + (offset & 31);
 }
 
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,

@@ -452,8 +452,8 @@ void Stage::check_sizes() {
     fail(HLLM_INCOMPATIBLE_WORKER, "model dimensions exceed this worker's limits");
   if (c.kv_block_tokens && (c.kv_block_tokens & (c.kv_block_tokens - 1)))
     fail(HLLM_INVALID_REQUEST, "KV block tokens must be a power of two");
-  if (c.kv_block_tokens && c.kv_block_tokens < 32 && c.execution_dtype == HLLM_DTYPE_F16)
-    fail(HLLM_INVALID_REQUEST, "KV blocks of an F16 stage hold at least 32 tokens");
+  if (c.kv_block_tokens && c.kv_block_tokens < 32)
+    fail(HLLM_INVALID_REQUEST, "KV blocks hold at least 32 tokens");
   if (c.max_pass_rows > (1u << 16)) fail(HLLM_INVALID_REQUEST, "max pass rows too large");
 }
 
@@ -696,9 +696,10 @@ void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values)
       for (uint64_t which = 0; which < 2; ++which)
         for (uint64_t hd = 0; hd < K_; ++hd)
           for (uint64_t d = 0; d < D_; ++d) {
-            // keys [head][position][dim], values transposed [head][dim][position]
-            const uint64_t i = which ? ((K_ + hd) * D_ + d) * bt + (p - p0)
-                                     : (hd * bt + (p - p0)) * D_ + d;
+            // keys [head][position][dim]; values [head][position / 32][dim][position % 32]
+            const uint64_t o = p - p0;
+            const uint64_t i = which ? (K_ + hd) * head_elems + ((o >> 5) * D_ + d) * 32 + (o & 31)
+                                     : (hd * bt + o) * D_ + d;
             float v;
             if (kv_f32_) {
               std::memcpy(&v, block.data() + i * 4, 4);

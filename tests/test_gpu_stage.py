@@ -4,7 +4,7 @@ through the C ABI.
 Tolerances: F32 execution 3e-5 and F16 execution 5e-3 on the tiny Transformers fixture
 (the reference's own CUDA-backend bars, hLLM tests/cpp/cuda_stage_test.cpp:102); synthetic
 Qwen3-shaped slices in F16 execution: max-abs <= 2e-2 and cosine >= 0.9999 against the F32
-CPU oracle; F32 execution (split-precision GEMMs, F32 KV): 1e-4.
+CPU oracle; F32 execution (split-precision GEMMs, F32 KV): |d| <= 1e-4 + 1e-4 |expected|.
 """
 import numpy as np
 import pytest
@@ -19,6 +19,14 @@ KV_BYTES = 256 << 20
 
 def _say(*what):
     print("[gpu-case]", *what, flush=True)
+
+
+def within(got, expect, execution):
+    """F16 execution: max-abs <= 2e-2; F32 execution: |d| <= 1e-4 + 1e-4 |expect|."""
+    got, expect = np.asarray(got), np.asarray(expect)
+    if execution == "f16":
+        return np.abs(got - expect).max() <= 2e-2
+    return bool(np.all(np.abs(got - expect) <= 1e-4 + 1e-4 * np.abs(expect)))
 
 
 def cosine(a, b):
@@ -131,9 +139,8 @@ def test_tiny_llama_greedy_matches_oracle(execution):
         out = st.execute([capi.item(seq, 1, 8 + step)], token_ids=[tokens[-1]], want_logits=True)
         tokens.append(int(out["tokens"][0]))
         logits.append(out["logits"][0])
-    tol = 1e-4 if execution == "f32" else 2e-2
     for a, b in zip(logits, expect_logits):
-        assert np.abs(a - b).max() <= tol
+        assert within(a, b, execution)
     assert tokens == expect
     st.close()
 
@@ -221,13 +228,12 @@ def test_qwen3_slice_ragged_batch_matches_oracle(execution):
     tr2 = []
     ost.execute(np.array(prompts[2][:64], np.uint64), 0, oseqs[2], tr2)
     oseqs[2].prefill_only = False
-    tol = 2e-2 if execution == "f16" else 1e-4
     got = out["trace"][-1]
     for (a, b), expect in zip(((0, 37), (37, 42), (42, 106)), (tr[1], tr1[1], tr2[1])):
         d = got[a:b]
-        assert np.abs(d - expect).max() <= tol and cosine(d, expect) >= 0.9999
-    assert np.abs(out["logits"][0] - tr[2]).max() <= tol
-    assert np.abs(out["logits"][1] - tr1[2]).max() <= tol
+        assert within(d, expect, execution) and cosine(d, expect) >= 0.9999
+    assert within(out["logits"][0], tr[2], execution)
+    assert within(out["logits"][1], tr1[2], execution)
     assert cosine(out["logits"][0], tr[2]) >= 0.9999
     if execution == "f32":
         assert int(out["tokens"][0]) == ref0[1] and int(out["tokens"][1]) == ref1[1]
@@ -241,7 +247,7 @@ def test_qwen3_slice_ragged_batch_matches_oracle(execution):
     e1 = ost.execute(np.array([int(out["tokens"][1])], np.uint64), 5, oseqs[1], tr_b)
     e2 = ost.execute(np.array(prompts[2][64:], np.uint64), 64, oseqs[2], tr_c)
     for got_l, exp_l in zip(out2["logits"], (tr[2], tr_b[2], tr_c[2])):
-        assert np.abs(got_l - exp_l).max() <= tol
+        assert within(got_l, exp_l, execution)
     if execution == "f32":
         assert [int(t) for t in out2["tokens"]] == [e0[1], e1[1], e2[1]]
     st.close()
@@ -376,7 +382,6 @@ def test_long_context_split_attention_matches_oracle(execution):
     rng = np.random.default_rng(3)
     prompt = rng.integers(0, shape.vocab, 1500).tolist()
     seq, oseq = st.allocate(1600), ost.allocate_sequence(1600)
-    tol = 2e-2 if execution == "f16" else 1e-4
     pos = 0
     while pos < len(prompt):
         take = min(512, len(prompt) - pos)
@@ -387,16 +392,16 @@ def test_long_context_split_attention_matches_oracle(execution):
         tr = []
         ref = ost.execute(np.array(prompt[pos:pos + take], np.uint64), pos, oseq, tr)
         got = out["trace"][-1]
-        assert np.abs(got - tr[1]).max() <= tol and cosine(got, tr[1]) >= 0.9999, pos
+        assert within(got, tr[1], execution) and cosine(got, tr[1]) >= 0.9999, pos
         pos += take
     oseq.prefill_only = False
-    assert np.abs(out["logits"][0] - tr[2]).max() <= tol
+    assert within(out["logits"][0], tr[2], execution)
     token = int(out["tokens"][0])
     for step in range(3):
         out = st.execute([capi.item(seq, 1, pos, from_device=True)], token_ids=[0], want_logits=True)
         tr = []
         ref = ost.execute(np.array([token], np.uint64), pos, oseq, tr)
-        assert np.abs(out["logits"][0] - tr[2]).max() <= tol
+        assert within(out["logits"][0], tr[2], execution)
         if execution == "f32":
             assert int(out["tokens"][0]) == ref[1]
         token = int(out["tokens"][0]) if execution == "f16" else ref[1]
