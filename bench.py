@@ -177,7 +177,7 @@ def decode_bench(stage, shape, rng, rows, steps):
     times, kv_read = [], 0
     for i in range(steps + 4):
         if i == steps:  # per-kernel HIP-event timing in 4 extra, untimed passes
-            stage.profile("gemm_,attention")
+            stage.profile("gemm_;attention")
         items["first_position"] = ctx
         t0 = time.perf_counter()
         capi.check(stage.lib.hllm_rocm_stage_execute(stage.handle, C.byref(p)))
@@ -185,8 +185,8 @@ def decode_bench(stage, shape, rng, rows, steps):
             times.append(time.perf_counter() - t0)
             kv_read += int((ctx + 1).sum())
         ctx += 1
-    fam = {f: stage.profile_read(f) for f in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
-                                              "gemm_lm_head", "attention")}
+    fam = {f: stage.profile_read(f)[:3] for f in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
+                                                  "gemm_lm_head", "attention")}
     stage.profile(None)
     for s in seqs:
         stage.release(s)
@@ -301,6 +301,9 @@ def main():
     ap.add_argument("--kv-block", type=int, default=0, help="tokens per KV block (0 = default)")
     ap.add_argument("--decode-only", action="store_true", help="only the pure-decode measurement")
     ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="end with three plain 1 GiB device copies (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU: the stage worker runs the whole model (or one "
@@ -333,15 +336,19 @@ def main():
         if i == max(0, args.warmup - 20):
             stage.profile("*")
         engine.step()
-    families = ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "gemm_lm_head", "attention",
-                "norm", "rope_append", "embed", "argmax", "pack")
-    prof = {f: stage.profile_read(f) for f in families}
-    dominant = max(prof, key=lambda f: prof[f][0])
+    records = stage.profile_records()
+    fam = {r: stage.profile_read(r) for r in records if "/" not in r and not r.startswith("k:")}
+    kern = {r[2:]: stage.profile_read(r) for r in records if r.startswith("k:")}
+    dominant = max(kern, key=lambda k: kern[k][0])
+    owners = sorted({r.split("/", 1)[0] for r in records if r.endswith("/" + dominant)})
     log("warmup kernel time (ms) by family:",
-        {f: round(v[0], 2) for f, v in sorted(prof.items(), key=lambda kv: -kv[1][0])})
-    log(f"active {len(engine.active)} waiting {len(engine.waiting)}; dominant kernel {dominant}")
+        {f: round(v[0], 2) for f, v in sorted(fam.items(), key=lambda kv: -kv[1][0])})
+    log("warmup kernel time (ms) by kernel:",
+        {k: round(v[0], 2) for k, v in sorted(kern.items(), key=lambda kv: -kv[1][0])[:8]})
+    log(f"active {len(engine.active)} waiting {len(engine.waiting)}; dominant kernel {dominant} "
+        f"(launched by {owners})")
 
-    stage.profile(dominant)
+    stage.profile(None)
     step_ms, tokens, rows_total, decode_rows = [], 0, 0, 0
     t_start = time.perf_counter()
     for i in range(args.steps):
@@ -352,14 +359,38 @@ def main():
         rows_total += r
         decode_rows += d
     elapsed = time.perf_counter() - t_start
-    dom_ms, dom_n, dom_bytes = stage.profile_read(dominant)
+    # Per-kernel roofline: HIP events around the dominant kernel's launches only, over a
+    # second region of the same length that continues the same workload (events perturb
+    # the host's launch rate, so the throughput region above runs without them).
+    stage.profile("k:" + dominant)
+    t_prof = time.perf_counter()
+    for i in range(args.steps):
+        engine.step()
+    prof_elapsed = time.perf_counter() - t_prof
+    dom_ms, dom_n, dom_bytes, dom_flops = stage.profile_read("k:" + dominant)
     stage.profile(None)
     log(f"timed {args.steps} steps in {elapsed:.3f}s: {tokens} tokens, {rows_total} rows "
         f"({decode_rows} decode rows)")
     engine.release_all()
 
     avg_launch_s = dom_ms / max(dom_n, 1) * 1e-3
-    achieved = (dom_bytes / max(dom_n, 1)) / avg_launch_s / 1e9 if dom_n else 0.0
+    # Bound: whichever peak the kernel's algorithmic work needs longer on.
+    t_hbm = dom_bytes / (HBM_PEAK_GBS * 1e9)
+    t_mfma = dom_flops / (MFMA_F16_PEAK_TFLOPS * 1e12)
+    if t_mfma > t_hbm:
+        achieved = dom_flops / max(dom_n, 1) / avg_launch_s / 1e12 if dom_n else 0.0
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_F16_PEAK_TFLOPS}
+    else:
+        achieved = dom_bytes / max(dom_n, 1) / avg_launch_s / 1e9 if dom_n else 0.0
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    roof.update({"traffic": measured_traffic(dominant), "kernel": dominant, "families": owners, "launches": dom_n,
+                 "region": f"{args.steps} further workload steps with HIP events on this kernel "
+                           f"({1e3 * prof_elapsed / args.steps:.2f} ms/step)",
+                 "avg_launch_us": avg_launch_s * 1e6,
+                 "algorithmic_bytes_per_launch": dom_bytes / max(dom_n, 1),
+                 "algorithmic_flops_per_launch": dom_flops / max(dom_n, 1)})
     result = {
         "metric": METRIC,
         "value": tokens / elapsed,
@@ -382,11 +413,7 @@ def main():
                    "decode_rows_per_step": decode_rows / args.steps},
         "latency_ms": {"p50": float(np.percentile(step_ms, 50)),
                        "p99": float(np.percentile(step_ms, 99))},
-        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "launches": dom_n,
-                     "avg_launch_us": avg_launch_s * 1e6,
-                     "algorithmic_bytes_per_launch": dom_bytes / max(dom_n, 1)},
+        "roofline": roof,
     }
     if not args.skip_extras:
         result["decode"] = decode_bench(stage, shape, rng, args.concurrency, args.decode_steps)
@@ -398,6 +425,45 @@ def main():
         mean_ctx = result.get("decode", {}).get("mean_context", 483.0)
         result["cpu_baseline"] = cpu_baseline(synthetic.QWEN3_4B, mean_ctx)
     print(json.dumps(result), flush=True)
+    if args.copy_calibration:
+        copy_calibration()
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter runs of this
+    workload (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter reads
+    for a 1 GiB device copy), or None when the kernel has not been measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get("kernels", {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return entry["bytes_per_launch"] if entry else None
+
+
+def copy_calibration():
+    """Three device-to-device copies of 1 GiB through the HIP runtime (its blit copy kernel):
+    a kernel whose HBM traffic is known (1 GiB read, 1 GiB written), profiled beside the
+    stage's kernels."""
+    hip = C.CDLL("libamdhip64.so")
+    n = 1 << 30
+    src, dst = C.c_void_p(), C.c_void_p()
+    for ptr in (src, dst):
+        if hip.hipMalloc(C.byref(ptr), C.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    try:
+        if hip.hipMemset(src, 1, C.c_size_t(n)) != 0:
+            raise RuntimeError("hipMemset failed")
+        for _ in range(3):
+            if hip.hipMemcpy(dst, src, C.c_size_t(n), 3) != 0:  # hipMemcpyDeviceToDevice
+                raise RuntimeError("hipMemcpy failed")
+        if hip.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipDeviceSynchronize failed")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    log("copy calibration: 3 x 1 GiB device-to-device copies")
 
 
 if __name__ == "__main__":

@@ -27,7 +27,8 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_allocate", "hllm_rocm_sequence_release",
            "hllm_rocm_sequence_length", "hllm_rocm_stage_execute", "hllm_rocm_stage_submit",
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
-           "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read")
+           "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
+           "hllm_rocm_stage_profile_records")
 
 
 class StageError(RuntimeError):
@@ -113,7 +114,9 @@ def library() -> C.CDLL:
     L.hllm_rocm_stage_read_tensor.argtypes = [vp, C.c_char_p, C.POINTER(C.c_float), u64]
     L.hllm_rocm_stage_profile.argtypes = [vp, C.c_char_p]
     L.hllm_rocm_stage_profile_read.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double),
-                                               C.POINTER(u64), C.POINTER(u64)]
+                                               C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                               C.POINTER(C.c_double)]
+    L.hllm_rocm_stage_profile_records.argtypes = [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if fn.restype is C.c_int or (fn.restype is None and name != "hllm_rocm_stage_destroy"):
@@ -277,14 +280,24 @@ class Stage:
 
     # --------------------------------------------------------------- profiling
     def profile(self, families: str | None) -> None:
-        """Time the named kernel families ("*" = all, None = off)."""
+        """Time the named families (';'-separated prefixes, "*" = all, "k:<kernel>" = one
+        kernel, None = off)."""
         check(self.lib.hllm_rocm_stage_profile(self.handle, families.encode() if families else None))
 
-    def profile_read(self, family: str):
-        ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
-        check(self.lib.hllm_rocm_stage_profile_read(self.handle, family.encode(), C.byref(ms),
-                                                    C.byref(n), C.byref(b)))
-        return ms.value, n.value, b.value
+    def profile_read(self, record: str):
+        """(milliseconds, launches, algorithmic bytes, algorithmic FLOPs) of a family record
+        or a "k:<kernel>" record ('*' suffix = prefix match)."""
+        ms, n, b, f = C.c_double(), C.c_uint64(), C.c_uint64(), C.c_double()
+        check(self.lib.hllm_rocm_stage_profile_read(self.handle, record.encode(), C.byref(ms),
+                                                    C.byref(n), C.byref(b), C.byref(f)))
+        return ms.value, n.value, b.value, f.value
+
+    def profile_records(self) -> list[str]:
+        need = C.c_uint64()
+        check(self.lib.hllm_rocm_stage_profile_records(self.handle, None, 0, C.byref(need)))
+        buf = C.create_string_buffer(need.value)
+        check(self.lib.hllm_rocm_stage_profile_records(self.handle, buf, need.value, C.byref(need)))
+        return [r for r in buf.value.decode().split("\n") if r]
 
 
 def item(sequence: int, query_tokens: int, first_position: int, sample: bool = True,

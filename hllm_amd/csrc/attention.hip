@@ -22,7 +22,6 @@
 namespace hllm_rocm {
 namespace {
 
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kTile = 256;
@@ -417,7 +416,7 @@ void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
     return true;
   }();
   (void)configured;
-  attention_mfma_kernel<D><<<dim3(a.work_count, a.kv_heads), kThreads, lds, stream>>>(a);
+  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_count, a.kv_heads), kThreads, lds, stream>>>(a); });
 }
 
 }  // namespace
@@ -440,11 +439,11 @@ void launch_attention(hipStream_t stream, const AttentionArgs& a) {
     const size_t lds = ((size_t)G * a.head_dim + (size_t)G * kTile + 2 * G) * sizeof(float);
     dim3 grid(a.rows, a.kv_heads, a.max_splits);
     if (a.kv.f32)
-      attention_valu_kernel<float><<<grid, kThreads, lds, stream>>>(a);
+      observed("attention_valu_kernel<float>", [&] { attention_valu_kernel<float><<<grid, kThreads, lds, stream>>>(a); });
     else
-      attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a);
+      observed("attention_valu_kernel<_Float16>", [&] { attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a); });
   }
-  attention_combine_kernel<<<dim3(a.rows, a.q_heads), 128, 0, stream>>>(a, mfma_path ? 1 : 0);
+  observed("attention_combine_kernel", [&] { attention_combine_kernel<<<dim3(a.rows, a.q_heads), 128, 0, stream>>>(a, mfma_path ? 1 : 0); });
 }
 
 }  // namespace hllm_rocm

@@ -29,9 +29,44 @@ inline void check_hip(hipError_t e, const char* what) {
 }
 #define HIP_CHECK(expr) ::hllm_rocm::check_hip((expr), #expr)
 
+// ------------------------------------------------------------------ launch observation
+//
+// Per-kernel timing: a stage that profiles installs an observer for the launches it issues
+// from its thread; every launcher brackets each kernel launch with `observed`, naming the
+// kernel as the profiler names it (template arguments included).
+struct LaunchObserver {
+  virtual void before(const char* kernel) = 0;
+  virtual void after(const char* kernel) = 0;
+
+ protected:
+  ~LaunchObserver() = default;
+};
+extern thread_local LaunchObserver* launch_observer;
+
+template <typename F>
+inline void observed(const char* kernel, F&& launch) {
+  LaunchObserver* o = launch_observer;
+  if (o) o->before(kernel);
+  launch();
+  if (o) o->after(kernel);
+}
+
+// "base<a, b, ...>" for integer template arguments, built once per instantiation.
+template <int... I>
+inline const char* kernel_name(const char* base) {
+  static const std::string name = [base] {
+    std::string s = std::string(base) + "<";
+    const int v[] = {I...};
+    for (size_t i = 0; i < sizeof...(I); ++i) s += (i ? ", " : "") + std::to_string(v[i]);
+    return s + ">";
+  }();
+  return name.c_str();
+}
+
 // ------------------------------------------------------------------ vectors
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ F-layout

@@ -213,24 +213,34 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   }
 }
 
-// Activation-staged variant: the workgroup's four waves split N (each owns NFW weight
-// fragment rows), the activation fragments of the tile are staged once per workgroup in LDS
-// (chunks of KC k-steps, double-buffered), and every wave streams its own weight fragments
-// through a ring of P k-steps. Activation traffic per weight byte drops to BM / BN.
+// Activation-staged variant for passes of many rows: the workgroup's four waves split N
+// (each owns NFW weight fragment rows, streamed from HBM through a ring of P k-steps), and
+// the activation fragments of the tile (BM = 16*MF rows) are staged once per workgroup in
+// LDS (chunks of KC k-steps, double-buffered) and read by all four waves, so activation
+// traffic per weight byte is BM / BN. Epilogues are applied straight from the accumulators.
+//
+// Block order is XCD-aware: id = split * slots + ((n_tile / 8) * m_tiles + m_tile) * 8 +
+// n_tile % 8, so all row tiles of one weight tile have the same id modulo 8 (one XCD, one
+// L2) and are dispatched together: the weight tile is read from HBM once.
 template <int MF, int NFW, int KC, int P, int PREC>
-__global__ void __launch_bounds__(256)
-    gemm_xlds_kernel(GemmArgs a, int n_tiles, int tiles) {
-  constexpr int BM = 16 * MF, BN = 64 * NFW, NT = 256, LDT = BN + 4;
+__global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
+    gemm_xlds_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
+  constexpr int BM = 16 * MF, BN = 64 * NFW, NT = 256;
   constexpr bool kLoA = PREC >= kSplitA, kLoB = PREC == kSplitAB;
   constexpr int XP = kLoA ? 2 : 1;                  // activation parts (hi, lo)
   constexpr int CHUNK = MF * KC * 64 * XP;          // half8s per staged chunk
+  static_assert(KC % P == 0, "the ring slot of a k-step must be a compile-time index");
   extern __shared__ float lds[];
   half8* xs = reinterpret_cast<half8*>(lds);        // [2][XP][MF][KC][64]
   const int M = a.device_m ? *a.device_m : a.M;
-  const int split = blockIdx.x / tiles;
-  const int tile = blockIdx.x - split * tiles;
-  const int tile_n = tile % n_tiles, tile_m = tile / n_tiles;
-  if (tile_m * BM >= M) return;
+  const int slots = n_groups * m_tiles * 8;
+  const int split = blockIdx.x / slots;
+  const int r = blockIdx.x - split * slots;
+  const int group_m = r >> 3;
+  const int group = group_m / m_tiles, tile_m = group_m - group * m_tiles;
+  const int tile_n = group * 8 + (r & 7);
+  if (tile_n >= n_tiles || tile_m * BM >= M) return;  // uniform over the workgroup
+  const int tile = tile_m * n_tiles + tile_n;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int KT = (int)(a.Kp >> 5);
   const int per = ((KT + a.ksplit - 1) / a.ksplit + KC - 1) / KC * KC;
@@ -243,19 +253,24 @@ __global__ void __launch_bounds__(256)
   const half8* X = reinterpret_cast<const half8*>(a.x_hi) + (size_t)mfrag0 * frag_stride;
   const half8* XL = reinterpret_cast<const half8*>(a.x_lo) + (size_t)mfrag0 * frag_stride;
 
-  floatx4 acc[MF][NFW], acc2[MF][NFW];
+  floatx4 acc[MF][NFW], acc2[kLoA ? MF : 1][kLoA ? NFW : 1];
 #pragma unroll
   for (int i = 0; i < MF; ++i)
 #pragma unroll
-    for (int j = 0; j < NFW; ++j) {
-      acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-      acc2[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < NFW; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (kLoA) {
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NFW; ++j) acc2[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
   const int steps = kt1 > kt0 ? kt1 - kt0 : 0;
   const int chunks = (steps + KC - 1) / KC;
 
   // Staging of chunk c (k-steps kt0 + c*KC ...) into buffer c % 2: thread-strided pieces.
-  constexpr int PIECES = CHUNK / NT > 0 ? (CHUNK + NT - 1) / NT : 1;
+  // Activation rows past the operand's padding are not read: the operand is padded to the
+  // tile height by the caller (gemm_tile_rows).
+  constexpr int PIECES = (CHUNK + NT - 1) / NT;
   half8 stage[PIECES];
   auto fetch_x = [&](int c) {
 #pragma unroll
@@ -302,27 +317,21 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < KC; ++j) {
       const int step = c * KC + j;
       if (step < steps) {
-        const int slot = j % P;  // P divides KC, so step % P == j % P (a register index)
-        half8 x[MF];
+        const int slot = j % P;  // P divides KC, so step % P == j % P
 #pragma unroll
-        for (int i = 0; i < MF; ++i) x[i] = xb[(i * KC + j) * 64 + lane];
+        for (int i = 0; i < MF; ++i) {
+          const half8 x = xb[(i * KC + j) * 64 + lane];
 #pragma unroll
-        for (int i = 0; i < MF; ++i)
-#pragma unroll
-          for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[slot][n], x[i], acc[i][n]);
-        if constexpr (kLoA) {
-#pragma unroll
-          for (int i = 0; i < MF; ++i) {
+          for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[slot][n], x, acc[i][n]);
+          if constexpr (kLoA) {
             const half8 xl = xb[MF * KC * 64 + (i * KC + j) * 64 + lane];
 #pragma unroll
             for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rb[slot][n], xl, acc2[i][n]);
           }
-        }
-        if constexpr (kLoB) {
+          if constexpr (kLoB) {
 #pragma unroll
-          for (int i = 0; i < MF; ++i)
-#pragma unroll
-            for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rbl[slot][n], x[i], acc2[i][n]);
+            for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rbl[slot][n], x, acc2[i][n]);
+          }
         }
         if (step + P < steps) load_w(slot, kt0 + step + P);
       }
@@ -331,65 +340,94 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
   }
 
-  // Output tile in LDS (reusing the staging area): each wave owns its columns.
-  float* tile_out = lds;
+  // Lane (q = lane / 16, t = lane % 16) of accumulator (i, n) holds row 16 i + t, features
+  // 16 n + 4 q .. + 3 of the wave's NFW * 16.
+  auto value = [&](int i, int n) {
+    floatx4 v = acc[i][n];
+    if constexpr (kLoA) {
+      v[0] += acc2[i][n][0] * kLoUnscale;
+      v[1] += acc2[i][n][1] * kLoUnscale;
+      v[2] += acc2[i][n][2] * kLoUnscale;
+      v[3] += acc2[i][n][3] * kLoUnscale;
+    }
+    return v;
+  };
+  const int q4 = (lane >> 4) * 4, t16 = lane & 15;
+  if (a.ksplit > 1) {
+    // Partial tile of this K split, summed in split order by gemm_reduce_kernel.
+    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
 #pragma unroll
-  for (int i = 0; i < MF; ++i)
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int n = 0; n < NFW; ++n)
+        *reinterpret_cast<floatx4*>(ws + (i * 16 + t16) * BN + (wave * NFW + n) * 16 + q4) = value(i, n);
+    return;
+  }
+  const int m_base = tile_m * BM;
+  if (a.epilogue == kEpiSwiglu) {
+    // A wave's features are whole 64-wide groups: 32 gate features (fragments 4g, 4g+1),
+    // then the 32 matching up features (fragments 4g+2, 4g+3).
+    static_assert(NFW % 4 == 0, "SwiGLU needs whole gate/up groups per wave");
+#pragma unroll
+    for (int gq = 0; gq < NFW / 4; ++gq) {
+      const uint64_t g = (uint64_t)(tile_n * BN + wave * NFW * 16) / 64 + gq;
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        const int row = m_base + i * 16 + t16;
+        if (row >= M) continue;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint64_t col = g * 32 + h * 16 + q4;
+          if (col >= a.out_cols_padded) continue;
+          const floatx4 gate = value(i, 4 * gq + h), up = value(i, 4 * gq + 2 + h);
+          half4 vh, vl;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float y = silu_mul(gate[t], up[t]);
+            vh[t] = to_half(y);
+            vl[t] = to_half((y - (float)vh[t]) * kLoScale);
+          }
+          const uint64_t at = flayout_index(row, col, a.out_cols_padded);
+          *reinterpret_cast<half4*>(a.out_hi + at) = vh;
+          if (a.out_lo) *reinterpret_cast<half4*>(a.out_lo + at) = vl;
+        }
+      }
+    }
+    return;
+  }
+  const bool vec = (a.ldo & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+    const int row = m_base + i * 16 + t16;
+    if (row >= M) continue;
 #pragma unroll
     for (int n = 0; n < NFW; ++n) {
-      floatx4 v = acc[i][n];
-      if constexpr (kLoA) {
-        v[0] += acc2[i][n][0] * kLoUnscale;
-        v[1] += acc2[i][n][1] * kLoUnscale;
-        v[2] += acc2[i][n][2] * kLoUnscale;
-        v[3] += acc2[i][n][3] * kLoUnscale;
-      }
-      const int m = i * 16 + (lane & 15);
-      const int col = (wave * NFW + n) * 16 + (lane >> 4) * 4;
-      *reinterpret_cast<floatx4*>(tile_out + m * LDT + col) = v;
-    }
-  __syncthreads();
-  if (a.ksplit > 1) {
-    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
-    for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
-      const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-      *reinterpret_cast<floatx4*>(ws + m * BN + n) = *reinterpret_cast<const floatx4*>(tile_out + m * LDT + n);
-    }
-    return;
-  }
-  const int m_base = tile_m * BM, n_base = tile_n * BN;
-  if (a.epilogue == kEpiSwiglu) {
-    constexpr int GROUPS = BN / 64;
-    for (int e = threadIdx.x; e < BM * GROUPS * 4; e += NT) {
-      const int m = e / (GROUPS * 4), g = (e / 4) % GROUPS, c8 = e % 4;
-      const uint64_t col = (uint64_t)(n_base / 64 + g) * 32 + c8 * 8;
-      if (m_base + m >= M || col >= a.out_cols_padded) continue;
-      half8 vh, vl;
+      const int col = tile_n * BN + (wave * NFW + n) * 16 + q4;
+      if (col >= a.N) continue;
+      float* out = a.out + (size_t)row * a.ldo + col;
+      const floatx4 v = value(i, n);
+      if (vec && col + 3 < a.N) {
+        floatx4* o4 = reinterpret_cast<floatx4*>(out);
+        if (a.epilogue == kEpiResidual) {
+          floatx4 s = *o4;
+          s[0] += v[0];
+          s[1] += v[1];
+          s[2] += v[2];
+          s[3] += v[3];
+          *o4 = s;
+        } else {
+          *o4 = v;
+        }
+      } else {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const float y = silu_mul(tile_out[m * LDT + g * 64 + c8 * 8 + t], tile_out[m * LDT + g * 64 + 32 + c8 * 8 + t]);
-        vh[t] = to_half(y);
-        vl[t] = to_half((y - (float)vh[t]) * kLoScale);
-      }
-      const uint64_t at = flayout_index(m_base + m, col, a.out_cols_padded);
-      *reinterpret_cast<half8*>(a.out_hi + at) = vh;
-      if (a.out_lo) *reinterpret_cast<half8*>(a.out_lo + at) = vl;
-    }
-    return;
-  }
-  for (int e = threadIdx.x; e < BM * (BN / 4); e += NT) {
-    const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-    const int gm = m_base + m;
-    if (gm >= M) continue;
-    float* out = a.out + (size_t)gm * a.ldo + n_base + n;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (n_base + n + t < a.N) {
-        const float v = tile_out[m * LDT + n + t];
-        if (a.epilogue == kEpiResidual)
-          out[t] += v;
-        else
-          out[t] = v;
+        for (int t = 0; t < 4; ++t) {
+          if (col + t < a.N) {
+            if (a.epilogue == kEpiResidual)
+              out[t] += v[t];
+            else
+              out[t] = v[t];
+          }
+        }
       }
     }
   }
@@ -474,8 +512,8 @@ void run(dim3 grid, int threads, size_t lds, hipStream_t stream, const GemmArgs&
     return true;
   }();
   (void)configured;
-  gemm_kernel<MF, NF, WM, WN, WK, P, PREC><<<grid, threads, lds, stream>>>(a, n_tiles, tiles,
-                                                                           tiles_padded);
+  observed(kernel_name<MF, NF, WM, WN, WK, P, PREC>("gemm_kernel"), [&] { gemm_kernel<MF, NF, WM, WN, WK, P, PREC><<<grid, threads, lds, stream>>>(a, n_tiles, tiles,
+                                                                           tiles_padded); });
 }
 
 template <int MF, int NF, int WM, int WN, int WK, int P>
@@ -512,7 +550,7 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
   }
   if (ksplit > 1) {
     const int64_t threads = (int64_t)tiles * BM * BN / 8;
-    gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles);
+    observed(kernel_name<BM, BN>("gemm_reduce_kernel"), [&] { gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles); });
   }
 }
 
@@ -522,6 +560,7 @@ void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int t
   constexpr int BM = 16 * MF, BN = 64 * NFW;
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
+  const int n_groups = (n_tiles + kXcds - 1) / kXcds;
   const int tiles = n_tiles * m_tiles;
   const int KT = (int)(a.Kp >> 5);
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
@@ -530,25 +569,31 @@ void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int t
   if ((size_t)tiles * ksplit * BM * BN > a.workspace_floats) ksplit = 1;
   a.ksplit = ksplit;
   const int xp = prec >= kSplitA ? 2 : 1;
-  const size_t lds = std::max((size_t)2 * MF * KC * 64 * xp * 16, (size_t)BM * (BN + 4) * sizeof(float));
-  dim3 grid(tiles * ksplit);
-  auto go = [&](auto kernel) {
-    static bool configured = false;
-    if (!configured) {
-      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    160 * 1024));
-      configured = true;
-    }
-    kernel<<<grid, 256, lds, stream>>>(a, n_tiles, tiles);
+  const size_t lds = (size_t)2 * MF * KC * 64 * xp * 16;
+  dim3 grid((unsigned)(ksplit * n_groups * m_tiles * kXcds));
+  auto go = [&](auto kernel, const char* name) {
+    static const bool configured = [kernel] {
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      return true;
+    }();
+    (void)configured;
+    observed(name, [&] { kernel<<<grid, 256, lds, stream>>>(a, n_tiles, m_tiles, n_groups); });
   };
   switch (prec) {
-    case kF16: go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>); break;
-    case kSplitA: go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitA>); break;
-    default: go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>); break;
+    case kF16:
+      go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>, kernel_name<MF, NFW, KC, P, kF16>("gemm_xlds_kernel"));
+      break;
+    case kSplitA:
+      go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitA>, kernel_name<MF, NFW, KC, P, kSplitA>("gemm_xlds_kernel"));
+      break;
+    default:
+      go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>, kernel_name<MF, NFW, KC, P, kSplitAB>("gemm_xlds_kernel"));
+      break;
   }
   if (ksplit > 1) {
     const int64_t threads = (int64_t)tiles * BM * BN / 8;
-    gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles);
+    observed(kernel_name<BM, BN>("gemm_reduce_kernel"), [&] { gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles); });
   }
 }
 
@@ -581,23 +626,23 @@ void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int 
     case 6:
       launch_config<4, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
       break;
-    case 7:  // activation-staged: BM 16 x BN 128
-      launch_xlds<1, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 7:  // activation-staged: BM 64 x BN 256
+      launch_xlds<4, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
-    case 8:  // BM 32 x BN 128
-      launch_xlds<2, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 8:  // BM 128 x BN 256, chunks of 2 k-steps, ring of 2
+      launch_xlds<8, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
-    case 9:  // BM 64 x BN 128
-      launch_xlds<4, 2, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 9:  // BM 128 x BN 256, chunks of 4, ring of 2
+      launch_xlds<8, 4, 4, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
-    case 10:  // BM 64 x BN 256
-      launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 10:  // BM 128 x BN 256, chunks of 4, ring of 4
+      launch_xlds<8, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
-    case 11:  // BM 128 x BN 128
-      launch_xlds<8, 2, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 11:  // BM 32 x BN 256
+      launch_xlds<2, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
-    case 12:  // BM 128 x BN 64
-      launch_xlds<8, 1, 8, 8>(stream, args, prec, rows_bound, cus * 5 / 8, forced_ksplit);
+    case 12:  // BM 64 x BN 256, chunks of 8, ring of 4
+      launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     default:
       launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);

@@ -4,6 +4,8 @@
 #include "kernels.hpp"
 
 namespace hllm_rocm {
+
+thread_local LaunchObserver* launch_observer = nullptr;
 namespace {
 
 constexpr int kBlock = 256;
@@ -454,33 +456,33 @@ __global__ void __launch_bounds__(kBlock) relayout_kernel(RelayoutArgs a) {
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
                  const int32_t* last_token, const int32_t* block_table, int table_width,
                  int block_tokens, PackOut out) {
-  pack_kernel<<<n_items, kBlock, 0, stream>>>(items, n_items, host_tokens, last_token, block_table,
-                                               table_width, block_tokens, out);
+  observed("pack_kernel", [&] { pack_kernel<<<n_items, kBlock, 0, stream>>>(items, n_items, host_tokens, last_token, block_table,
+                                               table_width, block_tokens, out); });
 }
 
 void launch_embed(hipStream_t stream, const uint16_t* table_hi, const uint16_t* table_lo,
                   uint64_t cols_padded, const int32_t* row_token, int rows, int hidden, float* h) {
-  embed_kernel<<<rows, kBlock, 0, stream>>>(table_hi, table_lo, cols_padded, row_token, hidden, h);
+  observed("embed_kernel", [&] { embed_kernel<<<rows, kBlock, 0, stream>>>(table_hi, table_lo, cols_padded, row_token, hidden, h); });
 }
 
 void launch_boundary_decode(hipStream_t stream, const uint16_t* in, int rows, int hidden, float* h) {
   const uint64_t n = (uint64_t)rows * hidden;
-  boundary_decode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(in, n, h);
+  observed("boundary_decode_kernel", [&] { boundary_decode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(in, n, h); });
 }
 
 void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hidden, uint16_t* out,
                             int32_t* flags) {
   const uint64_t n = (uint64_t)rows * hidden;
-  boundary_encode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(h, n, out,
-                                                                                      flags);
+  observed("boundary_encode_kernel", [&] { boundary_encode_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, stream>>>(h, n, out,
+                                                                                      flags); });
 }
 
 void launch_rmsnorm_flayout(hipStream_t stream, const float* h, int hidden, const int32_t* row_index,
                             int rows, const int32_t* device_rows, const float* weight, float eps,
                             uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
   if (rows <= 0) return;
-  rmsnorm_flayout_kernel<<<rows, kBlock, 0, stream>>>(h, hidden, row_index, rows, device_rows,
-                                                      weight, eps, out_hi, out_lo, cols_padded);
+  observed("rmsnorm_flayout_kernel", [&] { rmsnorm_flayout_kernel<<<rows, kBlock, 0, stream>>>(h, hidden, row_index, rows, device_rows,
+                                                      weight, eps, out_hi, out_lo, cols_padded); });
 }
 
 void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
@@ -488,29 +490,29 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
                             const float* rope_cos, const float* rope_sin, const int32_t* row_position,
                             const int32_t* row_slot, KvView kv, int layer, float* q_out) {
   const int heads = q_heads + 2 * kv_heads;
-  qkv_rope_append_kernel<<<dim3(rows, (heads + 3) / 4), kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
+  observed("qkv_rope_append_kernel", [&] { qkv_rope_append_kernel<<<dim3(rows, (heads + 3) / 4), kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
                                                       k_norm, eps, rope_cos, rope_sin, row_position,
-                                                      row_slot, kv, layer, q_out);
+                                                      row_slot, kv, layer, q_out); });
 }
 
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
                    int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
                    int32_t* flags) {
   if (max_rows <= 0) return;
-  argmax_partial_kernel<<<dim3(max_rows, parts), kBlock, 0, stream>>>(logits, device_rows, cols,
+  observed("argmax_partial_kernel", [&] { argmax_partial_kernel<<<dim3(max_rows, parts), kBlock, 0, stream>>>(logits, device_rows, cols,
                                                                       parts, part_val, part_idx,
-                                                                      flags);
-  argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens);
+                                                                      flags); });
+  observed("argmax_final_kernel", [&] { argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens); });
 }
 
 void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,
                           const int32_t* sample_count, const ItemMeta* items, int32_t* last_token) {
-  record_tokens_kernel<<<8, 128, 0, stream>>>(tokens, sample_item, sample_count, items, last_token);
+  observed("record_tokens_kernel", [&] { record_tokens_kernel<<<8, 128, 0, stream>>>(tokens, sample_item, sample_count, items, last_token); });
 }
 
 void launch_relayout(hipStream_t stream, const RelayoutArgs& a) {
   const uint64_t threads = a.rows * ((a.cols + 7) / 8);
-  relayout_kernel<<<(unsigned)((threads + kBlock - 1) / kBlock), kBlock, 0, stream>>>(a);
+  observed("relayout_kernel", [&] { relayout_kernel<<<(unsigned)((threads + kBlock - 1) / kBlock), kBlock, 0, stream>>>(a); });
 }
 
 }  // namespace hllm_rocm

@@ -71,6 +71,7 @@ struct PinnedMemory {
 struct Matrix {  // an F-layout weight: hi parts and optional lo parts
   DeviceMemory hi, lo;
   uint64_t rows_padded = 0, cols_padded = 0;
+  uint64_t cols = 0;  // the contraction length before padding
 };
 
 struct Layer {
@@ -98,7 +99,10 @@ struct Target {
 
 struct Profile {
   std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+  uint64_t launches = 0;
   uint64_t bytes = 0;
+  double flops = 0.0;
+  bool owns_events = true;  // kernel records share the events of their family record
 };
 
 constexpr int kMaxSplits = 16;
@@ -131,7 +135,8 @@ class Stage {
   void read_kv(uint32_t handle, uint32_t layer, float* keys, float* values);
   void read_tensor(const std::string& name, float* out, uint64_t elements);
   void set_profiling(const std::string& families);
-  void profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes);
+  void profile_read(const std::string& record, double* ms, uint64_t* launches, uint64_t* bytes, double* flops);
+  std::string profile_records();
 
  private:
   void check_sizes();
@@ -144,7 +149,8 @@ class Stage {
             int n, int epilogue, float* out, int ldo, uint16_t* out_hi, uint16_t* out_lo,
             uint64_t out_cols_padded);
   template <typename F>
-  void timed(const char* family, uint64_t bytes, F&& launch);
+  void timed(const char* family, uint64_t bytes, double flops, F&& launch);
+  hipEvent_t take_event();
   void fail_pass(const std::vector<uint32_t>& sequences);
 
   hllm_rocm_stage_config c_;
@@ -238,6 +244,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   auto matrix = [&](Matrix& m, uint64_t rows, uint64_t cols, const char* what) {
     m.rows_padded = pad_to(rows, 256);  // whole GEMM weight tiles (at most 256 features)
     m.cols_padded = pad32(cols);
+    m.cols = cols;
     const size_t bytes = m.rows_padded * m.cols_padded * 2;
     m.hi.allocate(bytes, what);
     HIP_CHECK(hipMemsetAsync(m.hi.ptr, 0, bytes, stream_));
@@ -715,73 +722,146 @@ void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values)
 
 // --------------------------------------------------------------------- profiling
 
+hipEvent_t Stage::take_event() {
+  if (event_pool_.empty()) {
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    return e;
+  }
+  hipEvent_t e = event_pool_.back();
+  event_pool_.pop_back();
+  return e;
+}
+
 template <typename F>
-void Stage::timed(const char* family, uint64_t bytes, F&& launch) {
-  bool selected = false;
+void Stage::timed(const char* family, uint64_t bytes, double flops, F&& launch) {
+  // Filters are family prefixes ("*" = all) or "k:<kernel>" (that kernel only, whichever
+  // family launches it).
+  bool family_selected = false, kernel_filters = false;
   if (profiling_) {
-    for (const auto& prefix : profile_filter_) {
-      if (prefix == "*" || std::strncmp(family, prefix.c_str(), prefix.size()) == 0) selected = true;
+    for (const auto& f : profile_filter_) {
+      if (f.compare(0, 2, "k:") == 0)
+        kernel_filters = true;
+      else if (f == "*" || std::strncmp(family, f.c_str(), f.size()) == 0)
+        family_selected = true;
     }
   }
-  if (!selected) {
+  if (!family_selected && !kernel_filters) {
     launch();
     return;
   }
-  auto take = [&] {
-    if (event_pool_.empty()) {
-      hipEvent_t e;
-      HIP_CHECK(hipEventCreate(&e));
-      return e;
+  // Events around every kernel the launch issues (the launchers report each one).
+  struct Observer final : LaunchObserver {
+    Stage* stage;
+    const char* family;
+    uint64_t bytes;
+    double flops;
+    bool all = false;  // every kernel of the launch, or only the filtered ones
+    int kernels = 0;
+    bool active = false;
+    hipEvent_t start = nullptr;
+    bool wanted(const char* kernel) const {
+      if (all) return true;
+      for (const auto& f : stage->profile_filter_)
+        if (f.compare(0, 2, "k:") == 0 && f.compare(2, std::string::npos, kernel) == 0) return true;
+      return false;
     }
-    hipEvent_t e = event_pool_.back();
-    event_pool_.pop_back();
-    return e;
-  };
-  hipEvent_t start = take(), stop = take();
-  HIP_CHECK(hipEventRecord(start, stream_));
-  launch();
-  HIP_CHECK(hipEventRecord(stop, stream_));
-  Profile& p = profiles_[family];
-  p.events.emplace_back(start, stop);
-  p.bytes += bytes;
+    void before(const char* kernel) override {
+      active = wanted(kernel);
+      if (!active) return;
+      start = stage->take_event();
+      HIP_CHECK(hipEventRecord(start, stage->stream_));
+    }
+    void after(const char* kernel) override {
+      if (!active) {
+        ++kernels;
+        return;
+      }
+      hipEvent_t stop = stage->take_event();
+      HIP_CHECK(hipEventRecord(stop, stage->stream_));
+      const bool first = kernels++ == 0;
+      Profile& f = stage->profiles_[family];
+      f.events.emplace_back(start, stop);
+      if (first) {
+        f.launches += 1;
+        f.bytes += bytes;
+        f.flops += flops;
+      }
+      for (const std::string& name : {std::string("k:") + kernel, std::string(family) + "/" + kernel}) {
+        Profile& k = stage->profiles_[name];
+        k.owns_events = false;
+        k.events.emplace_back(start, stop);
+        k.launches += 1;
+        if (first) {
+          k.bytes += bytes;
+          k.flops += flops;
+        }
+      }
+    }
+  } observer;
+  observer.stage = this;
+  observer.all = family_selected;
+  observer.family = family;
+  observer.bytes = bytes;
+  observer.flops = flops;
+  LaunchObserver* previous = launch_observer;
+  launch_observer = &observer;
+  try {
+    launch();
+  } catch (...) {
+    launch_observer = previous;
+    throw;
+  }
+  launch_observer = previous;
 }
 
 void Stage::set_profiling(const std::string& families) {
   std::lock_guard<std::mutex> lock(pass_mutex_);
   HIP_CHECK(hipStreamSynchronize(stream_));
   for (auto& [name, p] : profiles_)
-    for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
+    if (p.owns_events)
+      for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
   profiles_.clear();
   profile_filter_.clear();
   size_t start = 0;
   while (start <= families.size()) {
-    const size_t end = std::min(families.find(',', start), families.size());
+    const size_t end = std::min(families.find(';', start), families.size());
     if (end > start) profile_filter_.push_back(families.substr(start, end - start));
     start = end + 1;
   }
   profiling_ = !profile_filter_.empty();
 }
 
-void Stage::profile_read(const std::string& family, double* ms, uint64_t* launches, uint64_t* bytes) {
+void Stage::profile_read(const std::string& record, double* ms, uint64_t* launches, uint64_t* bytes,
+                         double* flops) {
   std::lock_guard<std::mutex> lock(pass_mutex_);
   HIP_CHECK(hipStreamSynchronize(stream_));
-  double total = 0.0;
+  const bool prefix = !record.empty() && record.back() == '*';
+  const std::string stem = prefix ? record.substr(0, record.size() - 1) : record;
+  double total = 0.0, f = 0.0;
   uint64_t n = 0, b = 0;
   for (auto& [name, p] : profiles_) {
-    if (!(name == family || (family.back() == '*' && name.compare(0, family.size() - 1, family, 0,
-                                                                  family.size() - 1) == 0)))
-      continue;
+    if (!(prefix ? name.compare(0, stem.size(), stem) == 0 : name == record)) continue;
     for (auto& e : p.events) {
       float t = 0.f;
       HIP_CHECK(hipEventElapsedTime(&t, e.first, e.second));
       total += t;
     }
-    n += p.events.size();
+    n += p.launches;
     b += p.bytes;
+    f += p.flops;
   }
   *ms = total;
   *launches = n;
   *bytes = b;
+  *flops = f;
+}
+
+std::string Stage::profile_records() {
+  std::lock_guard<std::mutex> lock(pass_mutex_);
+  std::string out;
+  for (auto& [name, p] : profiles_) out += name + "\n";
+  return out;
 }
 
 // --------------------------------------------------------------------- the pass
@@ -812,7 +892,8 @@ void Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, cons
   const uint64_t xbytes = (uint64_t)rows * w.cols_padded * 2 * (x_lo ? 2 : 1);
   const uint64_t obytes = epilogue == kEpiSwiglu ? (uint64_t)rows * (n / 2) * 2 * (out_lo ? 2 : 1)
                                                  : (uint64_t)rows * n * 4 * (epilogue == kEpiResidual ? 2 : 1);
-  timed(family, wbytes + xbytes + obytes, [&] { launch_gemm(stream_, a, prec_, rows, cus_); });
+  const double flops = 2.0 * rows * n * w.cols;
+  timed(family, wbytes + xbytes + obytes, flops, [&] { launch_gemm(stream_, a, prec_, rows, cus_); });
 }
 
 void Stage::fail_pass(const std::vector<uint32_t>& sequences) {
@@ -886,6 +967,20 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     std::memcpy(pin_boundary_.ptr, pass.boundary_in, count * 2);
   }
   if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+  // Algorithmic attention bytes of one layer: every item's keys and values read once,
+  // queries read and outputs written once.
+  // FLOPs: 4 * D per (query head, attended key) pair (scores and the value sum).
+  uint64_t attn_bytes = 0;
+  double attn_flops = 0.0;
+  {
+    const uint64_t kv_el = kv_f32_ ? 4 : 2;
+    for (uint32_t i = 0; i < n; ++i) {
+      const double q = pass.item[i].query_tokens, first = (double)pass.item[i].first_position;
+      attn_bytes += (pass.item[i].first_position + pass.item[i].query_tokens) * 2 * K_ * D_ * kv_el;
+      attn_flops += 4.0 * Q_ * D_ * (q * first + q * (q + 1) / 2);
+    }
+    attn_bytes += rows * Q_ * D_ * (4 + 2);
+  }
   int attn_work_count = 0;
   if (mfma_attention_) {
     for (uint32_t i = 0; i < n; ++i)
@@ -903,20 +998,20 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     if (c_.first_stage)
       HIP_CHECK(hipMemcpyAsync(host_tokens_dev_.ptr, host_tokens, R * sizeof(int32_t), hipMemcpyHostToDevice,
                                stream_));
-    timed("pack", 0, [&] {
+    timed("pack", 0, 0.0, [&] {
       launch_pack(stream_, items_dev_.as<ItemMeta>(), (int)n, host_tokens_dev_.as<int32_t>(),
                   last_token_.as<int32_t>(), block_table_.as<int32_t>(), table_width_, kv_.block_tokens, pack_);
     });
     float* h = h_.as<float>();
     if (c_.first_stage) {
-      timed("embed", (uint64_t)R * H_ * 6, [&] {
+      timed("embed", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_embed(stream_, embedding_.hi.as<uint16_t>(), w_f32_ ? embedding_.lo.as<uint16_t>() : nullptr,
                      embedding_.cols_padded, pack_.row_token, R, (int)H_, h);
       });
     } else {
       HIP_CHECK(hipMemcpyAsync(boundary_dev_.ptr, pin_boundary_.ptr, (size_t)R * H_ * 2, hipMemcpyHostToDevice,
                                stream_));
-      timed("boundary", (uint64_t)R * H_ * 6,
+      timed("boundary", (uint64_t)R * H_ * 6, 0.0,
             [&] { launch_boundary_decode(stream_, boundary_dev_.as<uint16_t>(), R, (int)H_, h); });
     }
     uint16_t* a0h = a0_hi_.as<uint16_t>();
@@ -929,13 +1024,13 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     for (uint64_t l = 0; l < L_; ++l) {
       if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
       Layer& w = *layers_[l];
-      timed("norm", (uint64_t)R * H_ * 6, [&] {
+      timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.input_norm.as<float>(), eps, a0h, a0l,
                                Hp_);
       });
       gemm("gemm_qkv", w.qkv, a0h, a0l, R, (int)qkv_n_, kEpiStore, qkv_.as<float>(), (int)qkv_n_, nullptr,
            nullptr, 0);
-      timed("rope_append", (uint64_t)R * qkv_n_ * 6, [&] {
+      timed("rope_append", (uint64_t)R * qkv_n_ * 6, 0.0, [&] {
         launch_qkv_rope_append(stream_, qkv_.as<float>(), R, (int)Q_, (int)K_, (int)D_,
                                c_.query_key_norm ? w.q_norm.as<float>() : nullptr,
                                c_.query_key_norm ? w.k_norm.as<float>() : nullptr, eps, rope_cos_.as<float>(),
@@ -965,9 +1060,9 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       at.out_hi = a1h;
       at.out_lo = a1l;
       at.out_cols_padded = QDp_;
-      timed("attention", 0, [&] { launch_attention(stream_, at); });
+      timed("attention", attn_bytes, attn_flops, [&] { launch_attention(stream_, at); });
       gemm("gemm_o", w.o, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0);
-      timed("norm", (uint64_t)R * H_ * 6, [&] {
+      timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.post_norm.as<float>(), eps, a0h, a0l,
                                Hp_);
       });
@@ -982,14 +1077,14 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     }
     if (c_.final_stage) {
       if (S > 0) {
-        timed("norm", (uint64_t)S * H_ * 6, [&] {
+        timed("norm", (uint64_t)S * H_ * 6, 0.0, [&] {
           launch_rmsnorm_flayout(stream_, h, (int)H_, pack_.sample_row, S, nullptr, final_norm_.as<float>(), eps,
                                  a0h, a0l, Hp_);
         });
         const Matrix& head = c_.tied_head ? embedding_ : head_;
         gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
              nullptr, 0);
-        timed("argmax", (uint64_t)S * V_ * 4, [&] {
+        timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
           launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
                         argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_.as<int32_t>());
         });
@@ -1002,7 +1097,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
                                    hipMemcpyDeviceToHost, stream_));
       }
     } else {
-      timed("boundary", (uint64_t)R * H_ * 6, [&] {
+      timed("boundary", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_boundary_encode(stream_, h, R, (int)H_, boundary_dev_.as<uint16_t>(), flags_.as<int32_t>());
       });
       HIP_CHECK(hipMemcpyAsync(pin_boundary_.ptr, boundary_dev_.ptr, (size_t)R * H_ * 2, hipMemcpyDeviceToHost,
@@ -1207,11 +1302,26 @@ hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, const char* families
   return guarded([&] { impl(stage).set_profiling(families ? families : ""); });
 }
 
-hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family, double* milliseconds,
-                                         uint64_t* launches, uint64_t* bytes) {
+hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* record, double* milliseconds,
+                                         uint64_t* launches, uint64_t* bytes, double* flops) {
   return guarded([&] {
-    if (!family || !milliseconds || !launches || !bytes) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
-    impl(stage).profile_read(family, milliseconds, launches, bytes);
+    if (!record || !milliseconds || !launches || !bytes || !flops)
+      hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).profile_read(record, milliseconds, launches, bytes, flops);
+  });
+}
+
+hllm_status hllm_rocm_stage_profile_records(hllm_rocm_stage* stage, char* buffer, uint64_t capacity,
+                                            uint64_t* needed) {
+  return guarded([&] {
+    if (!needed) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    const std::string names = impl(stage).profile_records();
+    *needed = names.size() + 1;
+    if (buffer && capacity) {
+      const uint64_t n = std::min<uint64_t>(capacity - 1, names.size());
+      std::memcpy(buffer, names.data(), n);
+      buffer[n] = 0;
+    }
   });
 }
 

@@ -180,14 +180,24 @@ hllm_status hllm_rocm_stage_read_tensor(hllm_rocm_stage* stage, const char* name
 hllm_status hllm_rocm_sequence_read_kv(hllm_rocm_stage* stage, uint32_t sequence, uint32_t layer,
                                        float* keys, float* values);
 
-/* Profiling hooks for benchmarks: HIP events on the stage's stream around every launch of
- * the kernel families named in `families` (comma-separated prefixes such as
- * "gemm_gate_up,attention"; "*" = all; NULL or "" = off), with the algorithmic bytes of
- * each launch; read back as sums per family (a trailing '*' matches a prefix). */
+/* Profiling hooks for benchmarks: HIP events on the stage's stream around every kernel
+ * launched for the operation families named in `families` (';'-separated prefixes such
+ * as "gemm_gate_up;attention"; "*" = all; "k:<kernel>" = that kernel only, whichever family
+ * launches it; NULL or "" = off). Each family launch carries its
+ * algorithmic HBM bytes and FLOPs. Records are kept per family (all kernels of the
+ * family's launches), per kernel under "k:<kernel>" (the kernel as rocprofv3 names it,
+ * with the bytes and FLOPs of the family launch attributed to its first kernel) and per
+ * (family, kernel) pair under "<family>/<kernel>". Read back
+ * as sums per record (a trailing '*' matches a prefix); `launches` counts family launches,
+ * or kernel launches for "k:" records. */
 hllm_status hllm_rocm_stage_profile(hllm_rocm_stage* stage, const char* families);
-hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* family,
+hllm_status hllm_rocm_stage_profile_read(hllm_rocm_stage* stage, const char* record,
                                          double* milliseconds, uint64_t* launches,
-                                         uint64_t* bytes);
+                                         uint64_t* bytes, double* flops);
+/* Names of the records collected so far, newline-separated, NUL-terminated in `buffer`
+ * (truncated to `capacity` bytes); `needed` receives the full length including the NUL. */
+hllm_status hllm_rocm_stage_profile_records(hllm_rocm_stage* stage, char* buffer,
+                                            uint64_t capacity, uint64_t* needed);
 
 #ifdef __cplusplus
 }
