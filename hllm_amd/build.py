@@ -1,4 +1,6 @@
-"""Builds libhllm_rocm.so (HIP kernels + stage runtime + C ABI) in-tree for gfx950."""
+"""Builds, in-tree: libhllm_rocm.so (HIP kernels + stage runtime + C ABI, gfx950),
+libhllm_rocm_host.so (the C++ stage-backend adapter, loader and scheduler over that ABI)
+and the host test program tests/host/host_tests.cpp (into _build/host_tests)."""
 from __future__ import annotations
 
 import os
@@ -47,7 +49,35 @@ def build(jobs: int = 4) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIBRARY)
+    build_host()
     return LIBRARY
+
+
+HOST = os.path.join(HERE, "host")
+HOST_LIBRARY = os.path.join(HERE, "libhllm_rocm_host.so")
+HOST_SOURCES = ["json.cpp", "safetensors.cpp", "dense_loader.cpp", "decode_batch.cpp", "sampling.cpp",
+                "scheduler.cpp", "rocm_stage.cpp"]
+HOST_TESTS = os.path.join(HERE, "_build", "host_tests")
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}"]
+
+
+def build_host() -> str:
+    """The host adapter library (links libhllm_rocm.so) and its test program."""
+    tmp = HOST_LIBRARY + ".tmp"
+    srcs = [os.path.join(HOST, s) for s in HOST_SOURCES]
+    r = subprocess.run([CXX, *CXXFLAGS, "-shared", "-o", tmp, *srcs, f"-L{HERE}", "-lhllm_rocm",
+                        "-Wl,-rpath,$ORIGIN", "-pthread"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host library build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, HOST_LIBRARY)
+    tests = os.path.join(ROOT, "tests", "host", "host_tests.cpp")
+    r = subprocess.run([CXX, *CXXFLAGS, "-o", HOST_TESTS + ".tmp", tests, f"-L{HERE}", "-lhllm_rocm_host",
+                        "-lhllm_rocm", f"-Wl,-rpath,$ORIGIN/..", "-pthread"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host test build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(HOST_TESTS + ".tmp", HOST_TESTS)
+    return HOST_LIBRARY
 
 
 if __name__ == "__main__":

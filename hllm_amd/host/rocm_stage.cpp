@@ -1,0 +1,296 @@
+#include "rocm_stage.hpp"
+
+#include <cstring>
+#include <limits>
+
+namespace hllm_rocm::backend {
+
+using runtime::Error;
+
+void check(hllm_status status) {
+  if (status == HLLM_OK) return;
+  const std::string message = hllm_rocm_last_error();
+  switch (status) {
+    case HLLM_INVALID_REQUEST: throw Error::invalid_request(message);
+    case HLLM_INCOMPATIBLE_WORKER: throw Error::incompatible_worker(message);
+    case HLLM_RESOURCE_EXHAUSTED: throw Error::resource_exhausted(message);
+    case HLLM_DEADLINE_EXCEEDED: throw Error::deadline_exceeded(message);
+    case HLLM_CANCELLED: throw Error::cancelled(message);
+    default: throw Error::internal(message);
+  }
+}
+
+namespace {
+
+// A sequence's paged KV blocks on the device; destroying the state returns them.
+struct RocmSequence final : runtime::SequenceState {
+  const RocmStage* owner{nullptr};
+  std::uint32_t handle{0};
+  std::size_t capacity{0};
+  std::size_t length{0};
+  bool failed{false};
+  ~RocmSequence() override {
+    if (owner) static_cast<void>(hllm_rocm_sequence_release(owner->handle(), handle));
+  }
+};
+
+bool greedy(const runtime::SamplingOptions& s) { return s.temperature == 0.0 && !s.return_logprobs; }
+
+std::uint32_t abi_dtype(runtime::DataType d) {
+  switch (d) {
+    case runtime::DataType::kF32: return HLLM_DTYPE_F32;
+    case runtime::DataType::kF16: return HLLM_DTYPE_F16;
+    case runtime::DataType::kBF16: return HLLM_DTYPE_BF16;
+    default: throw Error::incompatible_worker("unsupported tensor dtype");
+  }
+}
+
+hllm_rocm_stage_config config_of(const model::DenseSource& s, const StageOptions& o) {
+  hllm_rocm_stage_config c{};
+  c.abi_version = HLLM_ROCM_ABI_VERSION;
+  c.hidden_size = s.config.hidden_size;
+  c.intermediate_size = s.config.intermediate_size;
+  c.attention_heads = s.config.attention_heads;
+  c.key_value_heads = s.config.key_value_heads;
+  c.head_dimension = s.config.head_dimension;
+  c.maximum_sequence_length = s.config.maximum_sequence_length;
+  c.vocabulary_size = s.vocabulary_size;
+  c.rms_norm_epsilon = s.config.rms_norm_epsilon;
+  c.rope_theta = s.config.rope_theta;
+  c.query_key_norm = s.config.query_key_norm;
+  c.layer_start = s.layer_start;
+  c.layer_end = s.layer_end;
+  c.first_stage = s.first;
+  c.final_stage = s.final;
+  c.tied_head = s.tied_head;
+  c.execution_dtype = abi_dtype(s.execution_dtype);
+  c.weight_dtype = abi_dtype(s.weight_dtype);
+  c.device = o.device;
+  c.kv_cache_bytes = o.kv_cache_bytes;
+  c.kv_block_tokens = o.kv_block_tokens;
+  c.max_sequences = o.max_sequences;
+  c.max_pass_rows = o.max_pass_rows;
+  return c;
+}
+
+runtime::MemoryAmounts amounts(const hllm_rocm_memory& m) {
+  return {m.host_bytes, m.device_bytes, m.pinned_host_bytes, m.unified_bytes};
+}
+
+}  // namespace
+
+RocmStage::RocmStage(const model::DenseSource& source, const std::filesystem::path& root, const StageOptions& options)
+    : config_(config_of(source, options)) {
+  (void)root;
+  check(hllm_rocm_stage_create(&config_, &stage_));
+  try {
+    std::vector<unsigned char> payload;
+    for (const auto& [name, t] : source.tensors) {
+      const runtime::SafetensorsFile& file = source.files.at(t.file);
+      const runtime::TensorMetadata& meta = file.tensor(name);
+      payload.resize(meta.byte_length);
+      file.read(meta, 0, payload.data(), meta.byte_length);
+      std::vector<std::uint64_t> shape(t.shape.begin(), t.shape.end());
+      check(hllm_rocm_stage_load_tensor(stage_, name.c_str(), abi_dtype(t.dtype), shape.data(),
+                                        static_cast<std::uint32_t>(shape.size()), payload.data(), payload.size()));
+    }
+    check(hllm_rocm_stage_finalize(stage_));
+  } catch (...) {
+    hllm_rocm_stage_destroy(stage_);
+    stage_ = nullptr;
+    throw;
+  }
+}
+
+RocmStage::RocmStage(hllm_rocm_stage* stage, const hllm_rocm_stage_config& config) : stage_(stage), config_(config) {
+  if (!stage_) throw Error::internal("null stage");
+}
+
+RocmStage::~RocmStage() {
+  if (stage_) hllm_rocm_stage_destroy(stage_);
+}
+
+runtime::MemoryAmounts RocmStage::weight_memory() const {
+  hllm_rocm_memory m{};
+  check(hllm_rocm_stage_weight_memory(stage_, &m));
+  return amounts(m);
+}
+
+runtime::SequenceMemory RocmStage::sequence_memory(std::size_t tokens, std::size_t maximum_query_tokens) const {
+  if (tokens == 0 || tokens > maximum_tokens()) throw Error::invalid_request("request exceeds model context capacity");
+  hllm_rocm_memory cache{}, workspace{};
+  check(hllm_rocm_stage_sequence_memory(stage_, tokens, runtime::query_rows(tokens, maximum_query_tokens), &cache,
+                                        &workspace));
+  return {amounts(cache), amounts(workspace)};
+}
+
+std::unique_ptr<runtime::SequenceState> RocmStage::allocate_sequence(std::size_t tokens) const {
+  static_cast<void>(sequence_memory(tokens, tokens));
+  auto state = std::make_unique<RocmSequence>();
+  std::uint32_t handle = 0;
+  check(hllm_rocm_sequence_allocate(stage_, tokens, &handle));
+  state->owner = this;
+  state->handle = handle;
+  state->capacity = tokens;
+  return state;
+}
+
+std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, bool batch_outputs) const {
+  std::scoped_lock lock(mutex_);
+  const std::size_t n = members.size();
+  const std::size_t hidden = config_.hidden_size;
+  std::vector<hllm_rocm_item> items(n);
+  std::vector<RocmSequence*> states(n);
+  std::vector<std::uint64_t> ids;
+  std::vector<std::uint16_t> rows;
+  std::size_t total_rows = 0, host_sampled = 0;
+  for (std::size_t i = 0; i < n; ++i) {
+    auto* s = dynamic_cast<RocmSequence*>(members[i].state);
+    if (!s || s->owner != this || s->failed || members[i].position != s->length)
+      throw Error::invalid_request("ROCm sequence state or position is invalid");
+    for (std::size_t j = 0; j < i; ++j)
+      if (states[j] == s) throw Error::invalid_request("a pass holds each sequence once");
+    states[i] = s;
+    const auto* tokens = std::get_if<runtime::TokenInput>(members[i].input);
+    const auto* boundary = std::get_if<runtime::BoundaryActivation>(members[i].input);
+    const std::size_t count = tokens ? tokens->ids.size() : boundary->tokens;
+    if ((tokens != nullptr) != (config_.first_stage != 0) || count == 0 || members[i].position > s->capacity ||
+        count > s->capacity - members[i].position)
+      throw Error::invalid_request("invalid ROCm stage input or context capacity");
+    if (tokens) {
+      ids.insert(ids.end(), tokens->ids.begin(), tokens->ids.end());
+    } else {
+      if (boundary->width != hidden || boundary->payload.size() != count * hidden * 2)
+        throw Error::invalid_request("invalid ROCm boundary shape");
+      const std::size_t at = rows.size();
+      rows.resize(at + count * hidden);
+      std::memcpy(rows.data() + at, boundary->payload.data(), boundary->payload.size());
+    }
+    hllm_rocm_item& it = items[i];
+    it.sequence = s->handle;
+    it.query_tokens = static_cast<std::uint32_t>(count);
+    it.first_position = members[i].position;
+    it.top_p = 1.0;
+    if (config_.final_stage && !s->prefill_only) {
+      runtime::validate_sampling(s->sampling);
+      it.flags = HLLM_ITEM_SAMPLE;
+      if (!greedy(s->sampling)) ++host_sampled;
+    }
+    total_rows += count;
+  }
+  if (total_rows > std::numeric_limits<std::uint32_t>::max()) throw Error::invalid_request("pass too large");
+
+  hllm_rocm_pass pass{};
+  pass.items = static_cast<std::uint32_t>(n);
+  pass.item = items.data();
+  pass.token_ids = config_.first_stage ? ids.data() : nullptr;
+  pass.boundary_in = config_.first_stage ? nullptr : rows.data();
+  std::vector<std::uint64_t> tokens_out(n, 0);
+  std::vector<float> logits;
+  std::vector<std::uint16_t> boundary_out;
+  if (config_.final_stage) {
+    pass.tokens = tokens_out.data();
+    std::size_t sampled = 0;
+    for (const auto& it : items) sampled += (it.flags & HLLM_ITEM_SAMPLE) != 0;
+    if (host_sampled) {
+      logits.resize(sampled * config_.vocabulary_size);
+      pass.logits = logits.data();
+    }
+  } else {
+    boundary_out.resize(total_rows * hidden);
+    pass.boundary_out = boundary_out.data();
+  }
+  const hllm_status status = hllm_rocm_stage_execute(stage_, &pass);
+  if (status == HLLM_INTERNAL)
+    for (RocmSequence* s : states) s->failed = true;  // the pass may have written part of the caches
+  check(status);
+
+  std::vector<runtime::StageOutput> out;
+  out.reserve(n);
+  if (config_.final_stage) {
+    std::size_t sampled_row = 0;
+    for (std::size_t i = 0; i < n; ++i) {
+      RocmSequence* s = states[i];
+      if (!(items[i].flags & HLLM_ITEM_SAMPLE)) {
+        out.emplace_back(runtime::PrefillProgress{});
+        continue;
+      }
+      if (greedy(s->sampling)) {
+        out.emplace_back(runtime::SampledToken{tokens_out[i]});
+      } else {
+        const float* row = logits.data() + sampled_row * config_.vocabulary_size;
+        out.emplace_back(runtime::sample_token(row, config_.vocabulary_size, s->sampling, s->generated_index++));
+      }
+      ++sampled_row;
+    }
+  } else {
+    std::size_t row = 0;
+    if (!batch_outputs) {
+      runtime::BoundaryActivation b{total_rows, hidden, std::vector<std::byte>(total_rows * hidden * 2)};
+      std::memcpy(b.payload.data(), boundary_out.data(), b.payload.size());
+      out.emplace_back(std::move(b));
+    } else {
+      for (std::size_t i = 0; i < n; ++i) {
+        const std::size_t count = items[i].query_tokens;
+        runtime::BoundaryActivation b{count, hidden, std::vector<std::byte>(count * hidden * 2)};
+        std::memcpy(b.payload.data(), boundary_out.data() + row * hidden, b.payload.size());
+        row += count;
+        out.emplace_back(std::move(b));
+      }
+    }
+  }
+  for (std::size_t i = 0; i < n; ++i) states[i]->length += items[i].query_tokens;
+  return out;
+}
+
+runtime::StageOutput RocmStage::execute(runtime::StageInput input, std::size_t first_position,
+                                        runtime::SequenceState& state, const std::atomic_bool& cancelled) const {
+  if (cancelled.load()) throw std::runtime_error("request cancelled");
+  std::vector<Member> members{{&input, first_position, &state}};
+  auto out = run(members, false);
+  return std::move(out.front());
+}
+
+std::vector<runtime::StageOutput> RocmStage::execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const {
+  static_cast<void>(runtime::combine_decode_inputs(items));  // the contract's batch rules
+  // An in-flight batch is not preempted: a member's cancellation is its caller's to observe.
+  std::vector<Member> members;
+  members.reserve(items.size());
+  for (auto& item : items) members.push_back({&item.input, item.position, item.sequence});
+  return run(members, true);
+}
+
+std::vector<runtime::StageOutput> RocmStage::execute_mixed(std::vector<runtime::DecodeBatchItem> items) const {
+  if (items.empty()) throw Error::invalid_request("empty pass");
+  std::vector<Member> members;
+  members.reserve(items.size());
+  for (auto& item : items) {
+    if (!item.sequence) throw Error::invalid_request("pass member without a sequence");
+    members.push_back({&item.input, item.position, item.sequence});
+  }
+  return run(members, true);
+}
+
+BackendCapabilities RocmBackendFactory::capabilities() const {
+  BackendCapabilities c;
+  c.kind = "ROCM";
+  c.primary_memory_domain = "DEVICE";
+  c.architectures = {"llama.v1", "qwen3.v1"};
+  c.execution_dtypes = {"F16", "F32"};
+  c.detail = "hllm-rocm stage worker (gfx950, ABI " + std::to_string(hllm_rocm_abi_version()) + ")";
+  c.supports_mixed_precision = true;
+  return c;
+}
+
+std::unique_ptr<runtime::StageBackend> RocmBackendFactory::load(const model::LoadStageRequest& request,
+                                                                const std::filesystem::path& root,
+                                                                const runtime::MemoryAmounts& capacity) const {
+  model::DenseSource source = model::inspect_dense_stage(request, root);
+  if (source.resident_bytes > capacity.device_bytes)
+    throw Error::resource_exhausted("stage weights exceed the device memory budget");
+  if (source.largest_payload_bytes > capacity.host_bytes)
+    throw Error::resource_exhausted("largest tensor exceeds the host memory budget for loading");
+  return std::make_unique<RocmStage>(source, root, options_);
+}
+
+}  // namespace hllm_rocm::backend

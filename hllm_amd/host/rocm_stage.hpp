@@ -1,0 +1,94 @@
+// The MI355X stage as a StageBackend (cpp/include/hllm/runtime/stage_backend.hpp:69-107),
+// implemented over the C ABI of include/hllm_rocm.h, and its factory
+// (cpp/include/hllm/runtime/backend_factory.hpp:28-47). This is the adapter a reference
+// worker binary links in place of its CPU or CUDA stage.
+#pragma once
+
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "dense_loader.hpp"
+#include "hllm_rocm.h"
+#include "runtime.hpp"
+
+namespace hllm_rocm::backend {
+
+struct StageOptions {
+  int device{0};
+  std::size_t kv_cache_bytes{0};     // 0: 90% of free HBM after weights
+  std::uint32_t kv_block_tokens{0};  // 0: 64
+  std::uint32_t max_sequences{0};    // 0: 512
+  std::uint32_t max_pass_rows{0};    // 0: 2048
+};
+
+// Translates a failed C-ABI call into the runtime's error categories.
+void check(hllm_status status);
+
+class RocmStage final : public runtime::StageBackend {
+ public:
+  // Creates the device stage for an admitted dense source and uploads its tensors.
+  RocmStage(const model::DenseSource& source, const std::filesystem::path& root, const StageOptions& options);
+  // Takes ownership of a stage built directly through the C ABI (finalized).
+  RocmStage(hllm_rocm_stage* stage, const hllm_rocm_stage_config& config);
+  ~RocmStage() override;
+  RocmStage(const RocmStage&) = delete;
+  RocmStage& operator=(const RocmStage&) = delete;
+
+  runtime::MemoryAmounts weight_memory() const override;
+  std::size_t hidden_size() const override { return config_.hidden_size; }
+  std::size_t vocabulary_size() const override { return config_.vocabulary_size; }
+  std::size_t maximum_tokens() const override { return config_.maximum_sequence_length; }
+  runtime::SequenceMemory sequence_memory(std::size_t tokens, std::size_t maximum_query_tokens) const override;
+  using runtime::StageBackend::sequence_memory;
+  std::unique_ptr<runtime::SequenceState> allocate_sequence(std::size_t tokens) const override;
+  runtime::StageOutput execute(runtime::StageInput input, std::size_t first_position, runtime::SequenceState& state,
+                               const std::atomic_bool& cancelled) const override;
+  bool supports_decode_batch() const override { return true; }
+  std::vector<runtime::StageOutput> execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const override;
+
+  // One ragged pass over any mix of prefill chunks and one-token decode inputs of distinct
+  // sequences (the reference contract runs these as separate passes). Outputs in item order.
+  std::vector<runtime::StageOutput> execute_mixed(std::vector<runtime::DecodeBatchItem> items) const;
+
+  hllm_rocm_stage* handle() const { return stage_; }
+  const hllm_rocm_stage_config& config() const { return config_; }
+
+ private:
+  struct Member {
+    runtime::StageInput* input;
+    std::size_t position;
+    runtime::SequenceState* state;
+  };
+  std::vector<runtime::StageOutput> run(std::vector<Member>& members, bool batch_outputs) const;
+
+  hllm_rocm_stage* stage_{nullptr};
+  hllm_rocm_stage_config config_{};
+  mutable std::mutex mutex_;
+};
+
+struct BackendCapabilities {
+  std::string kind;                  // "ROCM" (proto/profile.proto Backend needs this value)
+  std::string primary_memory_domain; // "DEVICE"
+  std::vector<std::string> architectures;
+  std::vector<std::string> execution_dtypes;
+  std::string detail;
+  bool supports_mixed_precision{true};
+};
+
+class RocmBackendFactory {
+ public:
+  explicit RocmBackendFactory(StageOptions options = {}) : options_(options) {}
+  BackendCapabilities capabilities() const;
+  // Validates the request and the memory budget, then returns a complete stage (nothing
+  // is published on failure: the partially built stage is destroyed).
+  std::unique_ptr<runtime::StageBackend> load(const model::LoadStageRequest& request,
+                                              const std::filesystem::path& root,
+                                              const runtime::MemoryAmounts& capacity) const;
+
+ private:
+  StageOptions options_;
+};
+
+}  // namespace hllm_rocm::backend

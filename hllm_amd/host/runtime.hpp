@@ -1,0 +1,148 @@
+// The stage-backend contract the ROCm worker is a drop-in for, restated in this
+// repository's own namespace: the same type names, fields and error categories as the
+// reference runtime (cpp/include/hllm/runtime/stage_backend.hpp,
+// cpp/include/hllm/runtime/error.hpp, cpp/include/hllm/runtime/memory.hpp,
+// cpp/include/hllm/runtime/sampling.hpp), so an adapter in the reference tree is a field
+// copy between the two.
+#pragma once
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <variant>
+#include <vector>
+
+namespace hllm_rocm::runtime {
+
+// error.hpp:10-17
+enum class ErrorCode {
+  kInvalidRequest,
+  kIncompatibleWorker,
+  kResourceExhausted,
+  kDeadlineExceeded,
+  kCancelled,
+  kInternal,
+};
+
+// error.hpp:19-40: a category the worker services translate to wire codes.
+class Error : public std::runtime_error {
+ public:
+  Error(ErrorCode code, const std::string& message) : std::runtime_error(message), code_(code) {}
+  [[nodiscard]] ErrorCode code() const noexcept { return code_; }
+  static Error invalid_request(const std::string& m) { return {ErrorCode::kInvalidRequest, m}; }
+  static Error incompatible_worker(const std::string& m) { return {ErrorCode::kIncompatibleWorker, m}; }
+  static Error resource_exhausted(const std::string& m) { return {ErrorCode::kResourceExhausted, m}; }
+  static Error deadline_exceeded(const std::string& m) { return {ErrorCode::kDeadlineExceeded, m}; }
+  static Error cancelled(const std::string& m) { return {ErrorCode::kCancelled, m}; }
+  static Error internal(const std::string& m) { return {ErrorCode::kInternal, m}; }
+
+ private:
+  ErrorCode code_;
+};
+
+// memory.hpp:11-17, 46-49
+struct MemoryAmounts {
+  std::size_t host_bytes{0};
+  std::size_t device_bytes{0};
+  std::size_t pinned_host_bytes{0};
+  std::size_t unified_bytes{0};
+};
+struct SequenceMemory {
+  MemoryAmounts cache;
+  MemoryAmounts workspace;
+};
+
+// sampling.hpp:10-28
+struct SamplingOptions {
+  double temperature{0.0};
+  double top_p{1.0};
+  std::uint64_t top_k{0};
+  std::uint64_t seed{0};
+  bool return_logprobs{false};
+  std::uint32_t top_logprobs{0};
+};
+struct TokenLogProbability {
+  std::uint64_t token_id;
+  double logprob;
+};
+struct SampledToken {
+  std::uint64_t id{};
+  std::optional<double> logprob{};
+  std::vector<TokenLogProbability> top_logprobs{};
+};
+
+// stage_backend.hpp:20-58
+struct BoundaryActivation {
+  std::size_t tokens;
+  std::size_t width;
+  std::vector<std::byte> payload;  // row-major little-endian F16, tokens * width * 2 bytes
+};
+struct TokenInput {
+  std::vector<std::uint64_t> ids;
+};
+using StageInput = std::variant<TokenInput, BoundaryActivation>;
+struct PrefillProgress {};
+using StageOutput = std::variant<BoundaryActivation, SampledToken, PrefillProgress>;
+
+struct SequenceState {
+  SamplingOptions sampling;
+  bool prefilling{false};
+  bool prefill_only{false};
+  std::uint64_t generated_index{0};
+  virtual ~SequenceState() = default;
+};
+
+struct DecodeBatchItem {
+  StageInput input;
+  std::size_t position;
+  SequenceState* sequence;
+  const std::atomic_bool* cancelled;
+};
+// decode_batch.cpp: one-token members in item order, at most 64, independent and ready.
+StageInput combine_decode_inputs(const std::vector<DecodeBatchItem>& items);
+std::vector<StageOutput> split_decode_boundary(BoundaryActivation output);
+
+// stage_backend.hpp:62-67
+[[nodiscard]] constexpr std::size_t query_rows(std::size_t tokens, std::size_t maximum_query_tokens) noexcept {
+  return maximum_query_tokens == 0 || maximum_query_tokens > tokens ? tokens : maximum_query_tokens;
+}
+
+// stage_backend.hpp:69-107
+class StageBackend {
+ public:
+  virtual ~StageBackend() = default;
+  [[nodiscard]] virtual MemoryAmounts weight_memory() const = 0;
+  [[nodiscard]] virtual std::size_t hidden_size() const = 0;
+  [[nodiscard]] virtual std::size_t vocabulary_size() const = 0;
+  [[nodiscard]] virtual std::size_t maximum_tokens() const = 0;
+  [[nodiscard]] virtual SequenceMemory sequence_memory(std::size_t tokens,
+                                                       std::size_t maximum_query_tokens) const = 0;
+  [[nodiscard]] SequenceMemory sequence_memory(std::size_t tokens) const {
+    return sequence_memory(tokens, tokens);
+  }
+  [[nodiscard]] virtual std::unique_ptr<SequenceState> allocate_sequence(std::size_t tokens) const = 0;
+  [[nodiscard]] virtual StageOutput execute(StageInput input, std::size_t first_position,
+                                            SequenceState& state,
+                                            const std::atomic_bool& cancelled) const = 0;
+  virtual bool supports_decode_batch() const { return false; }
+  virtual std::vector<StageOutput> execute_decode_batch(std::vector<DecodeBatchItem> items) const {
+    std::vector<StageOutput> outputs;
+    for (auto& item : items)
+      outputs.push_back(execute(std::move(item.input), item.position, *item.sequence, *item.cancelled));
+    return outputs;
+  }
+};
+
+// sampling.cpp:19-89 restated on the host (the device samples greedily; requests with a
+// temperature or log-probabilities are finished here from the stage's logits).
+void validate_sampling(const SamplingOptions& options);
+std::uint64_t sample_logits(const float* logits, std::size_t count, const SamplingOptions& options,
+                            std::uint64_t generated_index);
+SampledToken sample_token(const float* logits, std::size_t count, const SamplingOptions& options,
+                          std::uint64_t generated_index);
+
+}  // namespace hllm_rocm::runtime

@@ -11,6 +11,12 @@
 #include <string.h>
 #include <unistd.h>
 
+/* Planted mistakes, for the tests that show the oracle's checks catch them: 0 = none,
+ * 1 = residual after attention dropped, 2 = RoPE rotation sign flipped, 3 = causal mask
+ * excludes the query's own position (off by one), 4 = SwiGLU gates the wrong half,
+ * 5 = RMSNorm without epsilon inside the root but over n - 1 (a wrong mean). */
+int orc_planted_mistake = 0;
+
 /* ---------------------------------------------------------------- F16 / BF16 */
 
 /* cpp/src/half.cpp:8-34 */
@@ -122,7 +128,8 @@ void orc_rms_norm(const float* input, size_t rows, size_t columns, const float* 
     const float* x = input + r * columns;
     float squares = 0.0f;
     for (size_t c = 0; c < columns; ++c) squares += x[c] * x[c];
-    const float inverse = 1.0f / sqrtf(squares / (float)columns + epsilon);
+    const float n = orc_planted_mistake == 5 ? (float)(columns - 1) : (float)columns;
+    const float inverse = 1.0f / sqrtf(squares / n + epsilon);
     for (size_t c = 0; c < columns; ++c) output[r * columns + c] = x[c] * inverse * weights[c];
   }
 }
@@ -230,8 +237,13 @@ int orc_apply_rope(float* values, size_t rows, size_t heads, size_t head_dimensi
         const float s = sinf(angle);
         const float a = v[i];
         const float b = v[half + i];
-        v[i] = a * c - b * s;
-        v[half + i] = b * c + a * s;
+        if (orc_planted_mistake == 2) {
+          v[i] = a * c + b * s;
+          v[half + i] = b * c - a * s;
+        } else {
+          v[i] = a * c - b * s;
+          v[half + i] = b * c + a * s;
+        }
       }
     }
   }
@@ -284,7 +296,7 @@ void orc_attention(const float* queries, size_t rows, const orc_config* config,
   const float scale = 1.0f / sqrtf((float)D);
   float* scores = (float*)malloc((first_position + rows) * sizeof(float));
   for (size_t t = 0; t < rows; ++t) {
-    const size_t last = first_position + t;
+    const size_t last = first_position + t - (orc_planted_mistake == 3 && first_position + t > 0);
     for (size_t qh = 0; qh < config->attention_heads; ++qh) {
       const size_t kvh = qh / group;
       const float* q = queries + t * width + qh * D;
@@ -354,14 +366,15 @@ int orc_transformer_layer(const float* input, size_t rows, const orc_layer* laye
   if (status == ORC_OK) {
     orc_attention(q, rows, config, first_position, cache, attended);
     orc_linear(attended, rows, qw, layer->attention_output, H, output);
-    for (size_t i = 0; i < rows * H; ++i) output[i] += input[i];
+    if (orc_planted_mistake != 1)
+      for (size_t i = 0; i < rows * H; ++i) output[i] += input[i];
     orc_rms_norm(output, rows, H, layer->post_attention_norm, config->rms_norm_epsilon,
                  normalized);
     orc_linear(normalized, rows, H, layer->gate, I, gated);
     orc_linear(normalized, rows, H, layer->up, I, up);
     for (size_t i = 0; i < rows * I; ++i) {
-      const float g = gated[i];
-      gated[i] = (g / (1.0f + expf(-g))) * up[i];
+      const float g = orc_planted_mistake == 4 ? up[i] : gated[i];
+      gated[i] = (g / (1.0f + expf(-g))) * (orc_planted_mistake == 4 ? gated[i] : up[i]);
     }
     orc_linear(gated, rows, I, layer->down, H, down);
     for (size_t i = 0; i < rows * H; ++i) output[i] += down[i];

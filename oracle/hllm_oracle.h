@@ -142,6 +142,10 @@ void orc_synth_f16(uint64_t seed, uint64_t tensor_id, uint64_t first, size_t cou
                    float mean, float sigma, uint16_t* out);
 uint64_t orc_splitmix64(uint64_t state);
 
+/* Test switch: a nonzero value plants one of the numbered formula mistakes described in
+ * hllm_oracle.c, so tests can show the golden checks catch them. */
+extern int orc_planted_mistake;
+
 #ifdef __cplusplus
 }
 #endif

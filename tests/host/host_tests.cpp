@@ -1,0 +1,673 @@
+// Tests of the host-side stage contract (hllm_amd/host): JSON and Safetensors readers,
+// stage admission, decode-batch packing, host sampling, the pass scheduler, and (on a GPU)
+// the RocmStage adapter over the C ABI. Run one case per process:
+//   host_tests --list | host_tests <case> [args...]
+// Scheduler cases follow the reference's tests/cpp/scheduler_test.cpp; decode-batch cases
+// follow tests/cpp/decode_batch_contract.hpp.
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <future>
+#include <map>
+#include <sstream>
+#include <thread>
+
+#include "dense_loader.hpp"
+#include "json.hpp"
+#include "rocm_stage.hpp"
+#include "runtime.hpp"
+#include "safetensors.hpp"
+#include "scheduler.hpp"
+
+using namespace hllm_rocm;
+using namespace std::chrono_literals;
+namespace fs = std::filesystem;
+
+namespace {
+
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+#define CHECK(cond)                                                                               \
+  do {                                                                                            \
+    if (!(cond)) throw Failure(std::string(__FILE__) + ":" + std::to_string(__LINE__) + ": " #cond); \
+  } while (0)
+
+template <class F>
+void expect_error(F&& f, runtime::ErrorCode code, const char* where) {
+  try {
+    f();
+  } catch (const runtime::Error& e) {
+    if (e.code() != code) throw Failure(std::string(where) + ": wrong error category: " + e.what());
+    return;
+  }
+  throw Failure(std::string(where) + ": no error raised");
+}
+#define EXPECT_ERROR(expr, code) expect_error([&] { (void)(expr); }, runtime::ErrorCode::code, #expr)
+
+template <class Predicate>
+bool wait_for(Predicate p) {
+  const auto until = std::chrono::steady_clock::now() + 2s;
+  while (!p() && std::chrono::steady_clock::now() < until) std::this_thread::sleep_for(1ms);
+  return p();
+}
+
+fs::path scratch_dir(const char* name) {
+  const fs::path p = fs::temp_directory_path() / (std::string("hllm_host_") + name + "_" + std::to_string(::getpid()));
+  fs::remove_all(p);
+  fs::create_directories(p);
+  return p;
+}
+
+// Writes a Safetensors file: `header` is the JSON text, `data` the data section.
+void write_raw(const fs::path& path, const std::string& header, const std::string& data) {
+  std::ofstream out(path, std::ios::binary);
+  std::uint64_t n = header.size();
+  for (int b = 0; b < 8; ++b) out.put(static_cast<char>((n >> (8 * b)) & 0xff));
+  out << header << data;
+}
+
+struct Tensor {
+  std::string name, dtype;
+  std::vector<std::size_t> shape;
+  std::string bytes;
+};
+void write_safetensors(const fs::path& path, const std::vector<Tensor>& tensors) {
+  std::ostringstream h;
+  std::string data;
+  h << "{\"__metadata__\":{\"format\":\"pt\"}";
+  for (const Tensor& t : tensors) {
+    h << ",\"" << t.name << "\":{\"dtype\":\"" << t.dtype << "\",\"shape\":[";
+    for (std::size_t i = 0; i < t.shape.size(); ++i) h << (i ? "," : "") << t.shape[i];
+    h << "],\"data_offsets\":[" << data.size() << "," << data.size() + t.bytes.size() << "]}";
+    data += t.bytes;
+  }
+  h << "}";
+  write_raw(path, h.str(), data);
+}
+std::string f32_bytes(std::size_t n, float v) {
+  std::string s(n * 4, '\0');
+  for (std::size_t i = 0; i < n; ++i) std::memcpy(&s[i * 4], &v, 4);
+  return s;
+}
+
+// ------------------------------------------------------------------ JSON
+
+void json_reader() {
+  const json::Value v = json::parse(R"( {"a": [1, -2, 3.5e1, true, null], "s": "x\"\u00e9\ud83d\ude00", "big": 18446744073709551615} )");
+  CHECK(v.is_object());
+  const json::Value* a = v.find("a");
+  CHECK(a && a->array.size() == 5);
+  CHECK(a->array[0].is_unsigned && a->array[0].unsigned_value == 1);
+  CHECK(!a->array[1].is_unsigned && a->array[1].is_integer && a->array[1].signed_value == -2);
+  CHECK(!a->array[2].is_integer && a->array[2].number == 35.0);
+  CHECK(a->array[3].is_bool() && a->array[3].boolean && a->array[4].is_null());
+  CHECK(v.find("s")->string == "x\"\xc3\xa9\xf0\x9f\x98\x80");
+  CHECK(v.find("big")->unsigned_value == 18446744073709551615ull);
+  for (const char* bad : {"", "{", "[1,]", "{\"a\" 1}", "01", "1.", "\"\\x\"", "tru", "[1] 2", "\"\\ud800\""}) {
+    bool threw = false;
+    try {
+      json::parse(bad);
+    } catch (const json::ParseError&) {
+      threw = true;
+    }
+    CHECK(threw);
+  }
+}
+
+// ------------------------------------------------------------------ Safetensors
+
+void safetensors_reader() {
+  const fs::path dir = scratch_dir("st");
+  write_safetensors(dir / "ok.safetensors", {{"b", "F32", {2, 2}, f32_bytes(4, 1.5f)}, {"a", "F16", {3}, std::string(6, '\1')}});
+  runtime::SafetensorsFile f(dir / "ok.safetensors");
+  CHECK(f.tensors().size() == 2 && f.tensors()[0].name == "a");
+  const auto& b = f.tensor("b");
+  CHECK(b.dtype == runtime::DataType::kF32 && b.shape == (std::vector<std::size_t>{2, 2}) && b.byte_length == 16);
+  float vals[4];
+  f.read(b, 0, vals, 16);
+  CHECK(vals[3] == 1.5f);
+  EXPECT_ERROR(f.tensor("missing"), kIncompatibleWorker);
+  EXPECT_ERROR(f.read(b, 8, vals, 16), kIncompatibleWorker);
+  const std::pair<std::string, std::string> bad[] = {
+      {R"({"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}})", std::string(8, '\0')},     // length mismatch
+      {R"({"x":{"dtype":"Q4","shape":[2],"data_offsets":[0,8]}})", std::string(8, '\0')},      // dtype
+      {R"({"x":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},"y":{"dtype":"F32","shape":[1],"data_offsets":[4,8]}})",
+       std::string(8, '\0')},                                                                  // overlap
+      {R"({"x":{"dtype":"F32","shape":[4],"data_offsets":[0,16]}})", std::string(8, '\0')},    // past the end
+      {R"({"x":{"dtype":"F32","shape":[-1],"data_offsets":[0,4]}})", std::string(4, '\0')},    // negative dim
+      {R"({"x":{"dtype":"F32","shape":[1],"data_offsets":[4,0]}})", std::string(4, '\0')},     // reversed
+      {R"({"__metadata__":{}})", ""},                                                          // no tensors
+      {R"([1,2])", ""},                                                                        // not an object
+      {R"({"x":)", ""},                                                                        // invalid JSON
+  };
+  int i = 0;
+  for (const auto& [header, data] : bad) {
+    const fs::path p = dir / ("bad" + std::to_string(i++) + ".safetensors");
+    write_raw(p, header, data);
+    EXPECT_ERROR(runtime::SafetensorsFile(p), kIncompatibleWorker);
+  }
+  {
+    std::ofstream(dir / "short.safetensors") << "abc";
+    EXPECT_ERROR(runtime::SafetensorsFile(dir / "short.safetensors"), kIncompatibleWorker);
+    std::ofstream out(dir / "huge.safetensors", std::ios::binary);
+    const unsigned char prefix[8] = {0xff, 0xff, 0xff, 0xff, 0, 0, 0, 0};
+    out.write(reinterpret_cast<const char*>(prefix), 8);
+    out << "{}";
+  }
+  EXPECT_ERROR(runtime::SafetensorsFile(dir / "huge.safetensors"), kIncompatibleWorker);
+  fs::remove_all(dir);
+}
+
+// ------------------------------------------------------------------ stage admission
+
+// A two-layer Qwen3 checkpoint with zero-filled F32 weights (shapes only matter here).
+fs::path tiny_checkpoint(const char* name, bool tied) {
+  const fs::path dir = scratch_dir(name);
+  const std::size_t H = 8, I = 16, Q = 2, K = 1, D = 4, V = 32;
+  std::vector<Tensor> t;
+  auto add = [&](std::string n, std::vector<std::size_t> shape) {
+    std::size_t e = 1;
+    for (auto d : shape) e *= d;
+    t.push_back({std::move(n), "F32", shape, f32_bytes(e, 0.01f)});
+  };
+  add("model.embed_tokens.weight", {V, H});
+  add("model.norm.weight", {H});
+  if (!tied) add("lm_head.weight", {V, H});
+  for (int l = 0; l < 2; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    add(p + "input_layernorm.weight", {H});
+    add(p + "post_attention_layernorm.weight", {H});
+    add(p + "self_attn.q_proj.weight", {Q * D, H});
+    add(p + "self_attn.k_proj.weight", {K * D, H});
+    add(p + "self_attn.v_proj.weight", {K * D, H});
+    add(p + "self_attn.o_proj.weight", {H, Q * D});
+    add(p + "mlp.gate_proj.weight", {I, H});
+    add(p + "mlp.up_proj.weight", {I, H});
+    add(p + "mlp.down_proj.weight", {H, I});
+    add(p + "self_attn.q_norm.weight", {D});
+    add(p + "self_attn.k_norm.weight", {D});
+  }
+  write_safetensors(dir / "model.safetensors", t);
+  std::ofstream(dir / "config.json") << R"({"model_type":"qwen3","hidden_size":8,"intermediate_size":16,)"
+                                     << R"("num_hidden_layers":2,"num_attention_heads":2,"num_key_value_heads":1,)"
+                                     << R"("head_dim":4,"vocab_size":32,"max_position_embeddings":64,)"
+                                     << R"("rms_norm_eps":1e-6,"rope_theta":1000000.0,"hidden_act":"silu",)"
+                                     << R"("tie_word_embeddings":)" << (tied ? "true" : "false") << "}";
+  return dir;
+}
+
+model::LoadStageRequest request_for(const model::ModelManifest& m, std::uint32_t stage, std::uint32_t stages) {
+  model::LoadStageRequest r;
+  r.manifest = m;
+  r.stage_index = stage;
+  r.plan.execution_dtype = model::WireDType::kF16;
+  for (std::uint32_t s = 0; s < stages; ++s) {
+    model::StageAssignment a;
+    a.layer_start = s * m.config.num_layers / stages;
+    a.layer_end = (s + 1) * m.config.num_layers / stages;
+    a.owns_token_embedding = s == 0;
+    a.owns_final_norm = a.owns_lm_head = a.owns_sampling = s + 1 == stages;
+    r.plan.stages.push_back(a);
+  }
+  return r;
+}
+
+void dense_admission() {
+  const fs::path dir = tiny_checkpoint("adm", false);
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  CHECK(m.architecture.architecture_id == "qwen3.v1" && m.tensors.size() == 3 + 22);
+  const model::DenseSource whole = model::inspect_dense_stage(request_for(m, 0, 1), dir);
+  CHECK(whole.first && whole.final && !whole.tied_head && whole.tensors.size() == 25);
+  CHECK(whole.config.query_key_norm && whole.config.head_dimension == 4);
+  const model::DenseSource second = model::inspect_dense_stage(request_for(m, 1, 2), dir);
+  CHECK(!second.first && second.final && second.layer_start == 1 && second.tensors.size() == 11 + 2);
+  const model::DenseSource first = model::inspect_dense_stage(request_for(m, 0, 2), dir);
+  CHECK(first.first && !first.final && first.tensors.size() == 11 + 1);
+
+  auto mutated = [&](std::function<void(model::LoadStageRequest&)> change) {
+    model::LoadStageRequest r = request_for(m, 0, 1);
+    change(r);
+    return r;
+  };
+  const std::vector<std::function<void(model::LoadStageRequest&)>> incompatible = {
+      [](auto& r) { r.stage_index = 3; },
+      [](auto& r) { r.plan.execution_dtype = model::WireDType::kBF16; },
+      [](auto& r) { r.plan.weight_dtype = model::WireDType::kF16; },  // mixed needs schema 1.2 and F32 execution
+      [](auto& r) { r.manifest.architecture.architecture_id = "mistral.v1"; },
+      [](auto& r) { r.manifest.architecture.architecture_revision = "2"; },
+      [](auto& r) { r.manifest.architecture.feature_flags.push_back("sliding_window"); },
+      [](auto& r) { std::erase(r.manifest.architecture.feature_flags, std::string("qk_norm")); },
+      [](auto& r) { r.manifest.config.hidden_activation = "gelu"; },
+      [](auto& r) { r.manifest.config.has_rope_scaling = true; },
+      [](auto& r) { r.manifest.config.attention_bias = true; },
+      [](auto& r) { r.manifest.config.head_dim = 3; },
+      [](auto& r) { r.manifest.config.rms_norm_eps = 0.0; },
+      [](auto& r) { r.manifest.config.rope_theta = 1e300; },  // not finite as F32
+      [](auto& r) { r.plan.stages[0].layer_end = 5; },
+      [](auto& r) { r.plan.stages[0].owns_sampling = false; },
+      [](auto& r) { r.manifest.tensors.push_back(r.manifest.tensors[0]); },  // duplicate
+      [](auto& r) { r.manifest.tensors.erase(r.manifest.tensors.begin()); },  // missing
+      [](auto& r) { r.manifest.tensors[0].shape[0] += 1; },
+      [](auto& r) { r.manifest.tensors[0].data_offset += 4; },
+      [](auto& r) { r.manifest.tensors[0].dtype = model::WireDType::kF16; },
+      [](auto& r) { r.manifest.tensors[0].file = "../model.safetensors"; },
+      [](auto& r) { r.manifest.tensors[0].file = "/tmp/model.safetensors"; },
+      [](auto& r) {
+        for (auto& t : r.manifest.tensors)
+          if (t.role == model::TensorRole::kTransformerLayer) t.layer_index = 7;
+      },
+      [](auto& r) {
+        auto extra = r.manifest.tensors.back();
+        extra.name = "model.layers.0.self_attn.rotary.weight";
+        extra.layer_index = 0;
+        r.manifest.tensors.push_back(extra);
+      },
+  };
+  for (const auto& change : incompatible) EXPECT_ERROR(model::inspect_dense_stage(mutated(change), dir), kIncompatibleWorker);
+
+  const fs::path tied = tiny_checkpoint("adm_tied", true);
+  const model::ModelManifest mt = model::manifest_from_checkpoint(tied);
+  const model::DenseSource s2 = model::inspect_dense_stage(request_for(mt, 1, 2), tied);
+  CHECK(s2.tied_head && s2.tensors.count("model.embed_tokens.weight") && !s2.tensors.count("lm_head.weight"));
+  fs::remove_all(dir);
+  fs::remove_all(tied);
+}
+
+// ------------------------------------------------------------------ decode batches
+
+void decode_batch_packing() {
+  std::atomic_bool stop{false};
+  runtime::SequenceState a, b, busy;
+  busy.prefilling = true;
+  using Items = std::vector<runtime::DecodeBatchItem>;
+  auto tok = [](std::uint64_t id) { return runtime::StageInput{runtime::TokenInput{{id}}}; };
+  auto row = [](std::size_t width, std::byte fill) {
+    return runtime::StageInput{runtime::BoundaryActivation{1, width, std::vector<std::byte>(width * 2, fill)}};
+  };
+  const auto ids = std::get<runtime::TokenInput>(runtime::combine_decode_inputs(Items{{tok(5), 3, &a, &stop}, {tok(9), 1, &b, &stop}}));
+  CHECK(ids.ids == (std::vector<std::uint64_t>{5, 9}));
+  const auto rows = std::get<runtime::BoundaryActivation>(
+      runtime::combine_decode_inputs(Items{{row(3, std::byte{1}), 3, &a, &stop}, {row(3, std::byte{2}), 1, &b, &stop}}));
+  CHECK(rows.tokens == 2 && rows.width == 3 && rows.payload.size() == 12 && rows.payload[6] == std::byte{2});
+  const auto parts = runtime::split_decode_boundary(rows);
+  CHECK(parts.size() == 2 && std::get<runtime::BoundaryActivation>(parts[1]).payload[0] == std::byte{2});
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{}), kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 0, &a, &stop}}), kInvalidRequest);  // position 0
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &busy, &stop}}), kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &a, &stop}, {tok(2), 2, &a, &stop}}), kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &a, &stop}, {row(3, std::byte{0}), 2, &b, &stop}}),
+               kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{runtime::TokenInput{{1, 2}}, 2, &a, &stop}}), kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{row(3, std::byte{0}), 2, &a, &stop}, {row(4, std::byte{0}), 2, &b, &stop}}),
+               kInvalidRequest);
+  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, nullptr, &stop}}), kInvalidRequest);
+  std::vector<runtime::SequenceState> many(65);
+  Items big;
+  for (auto& s : many) big.push_back({tok(1), 1, &s, &stop});
+  EXPECT_ERROR(runtime::combine_decode_inputs(big), kInvalidRequest);
+  big.pop_back();
+  CHECK(std::get<runtime::TokenInput>(runtime::combine_decode_inputs(big)).ids.size() == 64);
+  EXPECT_ERROR(runtime::split_decode_boundary(runtime::BoundaryActivation{2, 3, std::vector<std::byte>(10)}), kInternal);
+}
+
+// ------------------------------------------------------------------ host sampling
+
+// Fixture written by tests/golden/make_sampling_vectors.py from the oracle (itself pinned
+// bitwise to the reference's sampling.cpp): logits, options, expected token / logprobs.
+void host_sampling(const std::vector<std::string>& args) {
+  CHECK(args.size() == 1);
+  std::ifstream in(args[0]);
+  std::stringstream text;
+  text << in.rdbuf();
+  const json::Value doc = json::parse(text.str());
+  int cases = 0;
+  std::vector<std::vector<float>> sets;
+  for (const json::Value& set : doc.find("logits")->array) {
+    sets.emplace_back();
+    for (const json::Value& v : set.array) sets.back().push_back(static_cast<float>(v.number));
+  }
+  for (const json::Value& c : doc.find("cases")->array) {
+    const std::vector<float>& logits = sets.at(c.find("logits_index")->unsigned_value);
+    runtime::SamplingOptions o;
+    o.temperature = c.find("temperature")->number;
+    o.top_p = c.find("top_p")->number;
+    o.top_k = c.find("top_k")->unsigned_value;
+    o.seed = c.find("seed")->unsigned_value;
+    o.return_logprobs = c.find("return_logprobs")->boolean;
+    o.top_logprobs = static_cast<std::uint32_t>(c.find("top_logprobs")->unsigned_value);
+    const auto got = runtime::sample_token(logits.data(), logits.size(), o, c.find("generated_index")->unsigned_value);
+    CHECK(got.id == c.find("token")->unsigned_value);
+    if (o.return_logprobs) {
+      CHECK(got.logprob && *got.logprob == c.find("logprob")->number);
+      const auto& tops = c.find("top_ids")->array;
+      CHECK(got.top_logprobs.size() == tops.size());
+      for (std::size_t i = 0; i < tops.size(); ++i) {
+        CHECK(got.top_logprobs[i].token_id == tops[i].unsigned_value);
+        CHECK(got.top_logprobs[i].logprob == c.find("top_values")->array[i].number);
+      }
+    }
+    ++cases;
+  }
+  CHECK(cases > 0);
+  const float bad[2] = {1.0f, NAN};
+  runtime::SamplingOptions o;
+  EXPECT_ERROR(runtime::sample_logits(bad, 2, o, 0), kInternal);
+  o.top_p = 0.0;
+  EXPECT_ERROR(runtime::sample_logits(bad, 1, o, 0), kInvalidRequest);
+  o = {};
+  o.top_logprobs = 2;  // without return_logprobs
+  EXPECT_ERROR(runtime::sample_logits(bad, 1, o, 0), kInvalidRequest);
+}
+
+// ------------------------------------------------------------------ scheduler
+
+class GateStage : public runtime::StageBackend {
+ public:
+  mutable std::mutex mutex;
+  mutable std::vector<std::uint64_t> order;
+  std::promise<void> release;
+  std::shared_future<void> gate = release.get_future().share();
+  bool supports_decode_batch() const override { return true; }
+  runtime::MemoryAmounts weight_memory() const override { return {}; }
+  std::size_t hidden_size() const override { return 1; }
+  std::size_t vocabulary_size() const override { return 1000; }
+  std::size_t maximum_tokens() const override { return 1024; }
+  runtime::SequenceMemory sequence_memory(std::size_t, std::size_t) const override { return {}; }
+  std::unique_ptr<runtime::SequenceState> allocate_sequence(std::size_t) const override {
+    return std::make_unique<runtime::SequenceState>();
+  }
+  runtime::StageOutput execute(runtime::StageInput input, std::size_t, runtime::SequenceState&,
+                               const std::atomic_bool&) const override {
+    const auto id = std::get<runtime::TokenInput>(input).ids.at(0);
+    if (id == 999) gate.wait();
+    std::scoped_lock lock(mutex);
+    order.push_back(id);
+    return runtime::SampledToken{id};
+  }
+};
+
+void scheduler_priority(std::size_t batch) {
+  worker::StageScheduler scheduler;
+  scheduler.configure(batch);
+  GateStage backend;
+  std::atomic_bool cancelled{false}, dropped{false};
+  auto execute = [&](std::uint64_t id, std::size_t position, const std::atomic_bool& stop) {
+    runtime::SequenceState sequence;
+    sequence.prefilling = id == 100;
+    return scheduler.execute(backend, runtime::TokenInput{{id}}, position, sequence, stop,
+                             std::chrono::system_clock::now() + 5s);
+  };
+  auto first = std::async(std::launch::async, [&] { return execute(999, 0, cancelled); });
+  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
+  std::vector<std::future<runtime::StageOutput>> decodes;
+  for (std::size_t i = 0; i < 10; ++i) {
+    decodes.push_back(std::async(std::launch::async, [&, i] { return execute(i, 1, cancelled); }));
+    CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == i + 1; }));
+  }
+  auto prefill = std::async(std::launch::async, [&] { return execute(100, 3, cancelled); });
+  auto dropped_job = std::async(std::launch::async, [&] {
+    try {
+      static_cast<void>(execute(200, 0, dropped));
+    } catch (const runtime::Error& e) {
+      return e.code() == runtime::ErrorCode::kCancelled;
+    }
+    return false;
+  });
+  CHECK(wait_for([&] { return scheduler.metrics().queued_prefills == 2; }));
+  dropped = true;
+  CHECK(wait_for([&] { return scheduler.metrics().queued_prefills == 1; }));
+  backend.release.set_value();
+  static_cast<void>(first.get());
+  for (auto& d : decodes) static_cast<void>(d.get());
+  static_cast<void>(prefill.get());
+  CHECK(dropped_job.get());
+  CHECK(backend.order == (std::vector<std::uint64_t>{999, 0, 1, 2, 3, 4, 5, 6, 7, 100, 8, 9}));
+  const auto m = scheduler.metrics();
+  CHECK(m.queued_prefills + m.queued_decodes + m.executing == 0);
+  CHECK(m.completed_steps == 12);
+  if (batch > 1) CHECK(m.decode_batches > 0 && m.largest_decode_batch == batch);
+}
+
+void scheduler_deadline() {
+  worker::StageScheduler scheduler;
+  GateStage backend;
+  std::atomic_bool stop{false};
+  runtime::SequenceState active, queued;
+  auto first = std::async(std::launch::async, [&] {
+    return scheduler.execute(backend, runtime::TokenInput{{999}}, 0, active, stop, std::chrono::system_clock::now() + 5s);
+  });
+  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
+  EXPECT_ERROR(scheduler.execute(backend, runtime::TokenInput{{1}}, 1, queued, stop,
+                                 std::chrono::system_clock::now() + 20ms),
+               kDeadlineExceeded);
+  CHECK(scheduler.metrics().queued_decodes == 0);
+  backend.release.set_value();
+  static_cast<void>(first.get());
+  CHECK(backend.order == (std::vector<std::uint64_t>{999}));
+}
+
+class BatchGateStage final : public GateStage {
+ public:
+  mutable std::promise<void> entered;
+  std::promise<void> finish;
+  std::shared_future<void> batch_gate = finish.get_future().share();
+  bool fail = false;
+  std::vector<runtime::StageOutput> execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const override {
+    entered.set_value();
+    if (batch_gate.wait_for(5s) != std::future_status::ready) throw std::runtime_error("test batch gate timed out");
+    if (fail) throw std::runtime_error("injected dispatch failure");
+    std::vector<runtime::StageOutput> result;
+    for (auto& item : items) {
+      item.sequence->generated_index += 1;
+      result.push_back(runtime::SampledToken{std::get<runtime::TokenInput>(item.input).ids[0]});
+    }
+    return result;
+  }
+};
+
+// A member cancelled while its batch runs still receives the batch's result (or its
+// failure); the scheduler accepts new work afterwards.
+void scheduler_in_flight(bool fail) {
+  worker::StageScheduler scheduler;
+  scheduler.configure(4);
+  BatchGateStage backend;
+  backend.fail = fail;
+  std::atomic_bool hold{false}, a_stop{false}, b_stop{false};
+  runtime::SequenceState gate_seq, a, b;
+  auto gate = std::async(std::launch::async, [&] {
+    return scheduler.execute(backend, runtime::TokenInput{{999}}, 0, gate_seq, hold, std::chrono::system_clock::now() + 5s);
+  });
+  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
+  auto run = [&](std::uint64_t id, runtime::SequenceState& s, std::atomic_bool& stop) {
+    return std::async(std::launch::async, [&, id] {
+      return scheduler.execute(backend, runtime::TokenInput{{id}}, 1, s, stop, std::chrono::system_clock::now() + 5s);
+    });
+  };
+  auto fa = run(1, a, a_stop);
+  CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == 1; }));
+  auto fb = run(2, b, b_stop);
+  CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == 2; }));
+  backend.release.set_value();
+  static_cast<void>(gate.get());
+  CHECK(backend.entered.get_future().wait_for(2s) == std::future_status::ready);
+  a_stop = true;  // cancelled while its batch is in flight
+  backend.finish.set_value();
+  if (fail) {
+    bool threw_a = false, threw_b = false;
+    try { static_cast<void>(fa.get()); } catch (const std::runtime_error&) { threw_a = true; }
+    try { static_cast<void>(fb.get()); } catch (const std::runtime_error&) { threw_b = true; }
+    CHECK(threw_a && threw_b);
+  } else {
+    CHECK(std::get<runtime::SampledToken>(fa.get()).id == 1);
+    CHECK(std::get<runtime::SampledToken>(fb.get()).id == 2);
+    CHECK(a.generated_index == 1 && b.generated_index == 1);
+  }
+  runtime::SequenceState c;
+  std::atomic_bool go{false};
+  const auto after = scheduler.execute(backend, runtime::TokenInput{{7}}, 0, c, go, std::chrono::system_clock::now() + 5s);
+  CHECK(std::get<runtime::SampledToken>(after).id == 7);
+  CHECK(scheduler.metrics().executing == 0);
+}
+
+void scheduler_configuration() {
+  worker::StageScheduler s;
+  EXPECT_ERROR(s.configure(0), kInvalidRequest);
+  EXPECT_ERROR(s.configure(65), kInvalidRequest);
+  s.configure(64);
+  s.configure(1);
+}
+
+// ------------------------------------------------------------------ GPU: the adapter
+
+// Loads a checkpoint directory through the factory and runs a greedy prefill then
+// `decodes` decode steps; prints the sampled tokens as a JSON list.
+void gpu_checkpoint_greedy(const std::vector<std::string>& args) {
+  CHECK(args.size() == 4);
+  const fs::path dir = args[0];
+  const std::string dtype = args[1];
+  std::vector<std::uint64_t> prompt;
+  {
+    std::stringstream s(args[2]);
+    std::string tok;
+    while (std::getline(s, tok, ',')) prompt.push_back(std::stoull(tok));
+  }
+  const int decodes = std::stoi(args[3]);
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  model::LoadStageRequest r = request_for(m, 0, 1);
+  r.plan.execution_dtype = dtype == "f32" ? model::WireDType::kF32 : model::WireDType::kF16;
+  backend::StageOptions options;
+  options.kv_cache_bytes = 64u << 20;
+  options.kv_block_tokens = 32;
+  options.max_sequences = 8;
+  options.max_pass_rows = 256;
+  backend::RocmBackendFactory factory(options);
+  runtime::MemoryAmounts capacity{1ull << 40, 1ull << 40, 0, 0};
+  auto stage = factory.load(r, dir, capacity);
+  std::atomic_bool stop{false};
+  auto seq = stage->allocate_sequence(prompt.size() + decodes + 1);
+  std::vector<std::uint64_t> out;
+  auto t = std::get<runtime::SampledToken>(stage->execute(runtime::TokenInput{prompt}, 0, *seq, stop)).id;
+  out.push_back(t);
+  for (int i = 0; i < decodes; ++i) {
+    t = std::get<runtime::SampledToken>(stage->execute(runtime::TokenInput{{t}}, prompt.size() + i, *seq, stop)).id;
+    out.push_back(t);
+  }
+  std::printf("TOKENS [");
+  for (std::size_t i = 0; i < out.size(); ++i) std::printf("%s%llu", i ? "," : "", static_cast<unsigned long long>(out[i]));
+  std::printf("]\n");
+  // State rules of the contract.
+  EXPECT_ERROR(stage->execute(runtime::TokenInput{{1}}, 0, *seq, stop), kInvalidRequest);  // wrong position
+  EXPECT_ERROR(stage->execute(runtime::TokenInput{{m.config.vocabulary_size}}, prompt.size() + decodes, *seq, stop),
+               kInvalidRequest);  // token ID outside the vocabulary
+  std::atomic_bool cancelled{true};
+  auto other = stage->allocate_sequence(4);
+  bool threw = false;
+  try {
+    static_cast<void>(stage->execute(runtime::TokenInput{{1}}, 0, *other, cancelled));
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  CHECK(threw);
+}
+
+// tests/cpp/decode_batch_contract.hpp: a decode batch returns what serial execution
+// returns, in item order, advancing each member's generated index, for greedy and
+// temperature sampling with log-probabilities.
+void gpu_decode_batch_contract(const std::vector<std::string>& args) {
+  CHECK(args.size() == 1);
+  const fs::path dir = args[0];
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  model::LoadStageRequest r = request_for(m, 0, 1);
+  r.plan.execution_dtype = model::WireDType::kF32;
+  backend::StageOptions options;
+  options.kv_cache_bytes = 64u << 20;
+  options.kv_block_tokens = 32;
+  options.max_sequences = 32;
+  options.max_pass_rows = 256;
+  backend::RocmBackendFactory factory(options);
+  auto stage = factory.load(r, dir, {1ull << 40, 1ull << 40, 0, 0});
+  CHECK(stage->supports_decode_batch());
+  for (double temperature : {0.0, 0.8}) {
+    std::atomic_bool cancelled{false};
+    std::vector<std::unique_ptr<runtime::SequenceState>> reference, batched;
+    const std::vector<std::size_t> lengths{7, 2, 4, 1};
+    std::vector<runtime::SampledToken> expected;
+    for (std::size_t i = 0; i < lengths.size(); ++i) {
+      reference.push_back(stage->allocate_sequence(lengths[i] + 1));
+      batched.push_back(stage->allocate_sequence(lengths[i] + 1));
+      for (auto* state : {reference.back().get(), batched.back().get()}) {
+        state->sampling = {temperature, 0.95, 8, i + 42, true, 3};
+        static_cast<void>(stage->execute(runtime::TokenInput{std::vector<std::uint64_t>(lengths[i], 1)}, 0, *state, cancelled));
+      }
+      expected.push_back(std::get<runtime::SampledToken>(
+          stage->execute(runtime::TokenInput{{4}}, lengths[i], *reference.back(), cancelled)));
+    }
+    std::vector<runtime::DecodeBatchItem> items;
+    for (std::size_t i = 0; i < lengths.size(); ++i)
+      items.push_back({runtime::TokenInput{{4}}, lengths[i], batched[i].get(), &cancelled});
+    const auto actual = stage->execute_decode_batch(std::move(items));
+    CHECK(actual.size() == expected.size());
+    for (std::size_t i = 0; i < expected.size(); ++i) {
+      const auto& token = std::get<runtime::SampledToken>(actual[i]);
+      CHECK(token.id == expected[i].id);
+      CHECK(token.logprob && expected[i].logprob && std::fabs(*token.logprob - *expected[i].logprob) < 0.02);
+      CHECK(token.top_logprobs.size() == 3);
+      CHECK(batched[i]->generated_index == reference[i]->generated_index);
+    }
+  }
+}
+
+struct Case {
+  const char* name;
+  std::function<void(const std::vector<std::string>&)> run;
+  bool gpu;
+};
+const std::vector<Case>& cases() {
+  static const std::vector<Case> all = {
+      {"json_reader", [](auto&) { json_reader(); }, false},
+      {"safetensors_reader", [](auto&) { safetensors_reader(); }, false},
+      {"dense_admission", [](auto&) { dense_admission(); }, false},
+      {"decode_batch_packing", [](auto&) { decode_batch_packing(); }, false},
+      {"host_sampling", host_sampling, false},
+      {"scheduler_priority_batch1", [](auto&) { scheduler_priority(1); }, false},
+      {"scheduler_priority_batch4", [](auto&) { scheduler_priority(4); }, false},
+      {"scheduler_deadline", [](auto&) { scheduler_deadline(); }, false},
+      {"scheduler_in_flight_ok", [](auto&) { scheduler_in_flight(false); }, false},
+      {"scheduler_in_flight_failure", [](auto&) { scheduler_in_flight(true); }, false},
+      {"scheduler_configuration", [](auto&) { scheduler_configuration(); }, false},
+      {"gpu_checkpoint_greedy", gpu_checkpoint_greedy, true},
+      {"gpu_decode_batch_contract", gpu_decode_batch_contract, true},
+  };
+  return all;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) {
+    std::fprintf(stderr, "usage: host_tests --list | <case> [args]\n");
+    return 2;
+  }
+  const std::string name = argv[1];
+  if (name == "--list") {
+    for (const Case& c : cases()) std::printf("%s %s\n", c.name, c.gpu ? "gpu" : "cpu");
+    return 0;
+  }
+  for (const Case& c : cases()) {
+    if (name != c.name) continue;
+    try {
+      c.run(std::vector<std::string>(argv + 2, argv + argc));
+    } catch (const std::exception& e) {
+      std::printf("FAIL %s: %s\n", c.name, e.what());
+      return 1;
+    }
+    std::printf("PASS %s\n", c.name);
+    return 0;
+  }
+  std::fprintf(stderr, "unknown case %s\n", name.c_str());
+  return 2;
+}

@@ -434,3 +434,22 @@ def test_planted_mistakes_are_caught():
     for mutate in mistakes:
         assert np.abs(run(mutate) - expect).max() > 1e-3
     assert base is not None
+
+
+@pytest.mark.parametrize("mistake", [1, 2, 3, 4, 5])
+def test_planted_formula_mistakes_fail_the_golden_vectors(mistake):
+    """Each formula mistake planted in the oracle (dropped residual, RoPE sign, causal
+    off-by-one, swapped SwiGLU halves, wrong RMS mean) fails the reference fixture."""
+    fx = models.tiny_reference()
+    x = models.tiny_rows(fx["embeddings"], 0, 5)
+    expect = models.tiny_rows(fx["layer_outputs"][1], 0, 5)
+    flag = C.c_int.in_dll(oracle.lib(), "orc_planted_mistake")
+    try:
+        flag.value = mistake
+        st = oracle.OracleStage(models.tiny_reference_stage())
+        got = st.forward(x, 0, st.allocate_sequence(32))
+    finally:
+        flag.value = 0
+    assert np.abs(got - expect).max() > 1e-3
+    st = oracle.OracleStage(models.tiny_reference_stage())
+    assert np.abs(st.forward(x, 0, st.allocate_sequence(32)) - expect).max() < 2e-5
