@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
   const bool split_keys = nvec <= 16;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int quad = lane >> 4, col = lane & 15;
   const int vf = split_keys ? 0 : wave;
   const int v = vf * 16 + col;
@@ -70,18 +70,12 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   const int seq = a.items[w.item].sequence;
   const int bt = a.kv.block_tokens, KVH = a.kv_heads;
   if (!split_keys && vf * 16 >= nvec) return;  // no __syncthreads on this path
-  // Physical blocks of the split: lane i holds the table entry of logical block chunk + i,
-  // refreshed every 64 blocks, so a tile's block is a lane read rather than a dependent
-  // global load. Tiles are 32-key aligned and blocks a multiple of 32 keys, so a tile lies
-  // in one block.
+  // A tile's physical block: a wave-uniform table entry, read through the scalar cache so
+  // that waiting for it never drains the vector loads of the tile in flight. Tiles are
+  // 32-key aligned and blocks a multiple of 32 keys, so a tile lies in one block.
   const int32_t* table = a.block_table + (size_t)seq * a.table_width;
-  int chunk = -64, chunk_entry = 0;
   auto block_of = [&](int logical) -> uint64_t {
-    if (logical - chunk >= 64) {  // wave-uniform: tiles only move forward
-      chunk = logical;
-      chunk_entry = chunk + lane < a.table_width ? table[chunk + lane] : 0;
-    }
-    return (uint64_t)(uint32_t)__shfl(chunk_entry, logical - chunk, 64);
+    return (uint64_t)(uint32_t)table[__builtin_amdgcn_readfirstlane(logical)];
   };
   const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
 
@@ -111,10 +105,8 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
     half8 k0[KK], k1[KK];
     half8 v[DF];
   };
-  auto fetch = [&](int t, Tile& f) {
-    const int logical = t / bt;
-    const uint64_t blk = block_of(logical);
-    const int off = t - logical * bt;
+  auto fetch = [&](int t, uint64_t blk, Tile& f) {
+    const int off = t % bt;
     const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
     const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
     // Key rows are permuted so that score fragment 0 row 4q+i is position 8q+i and fragment
@@ -131,12 +123,23 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       f.v[df] = *reinterpret_cast<const half8*>(vb + (size_t)(16 * df + col) * 32 + 8 * quad);
     }
   };
+  // Loads are issued unconditionally (a tile past the range re-reads the range's last
+  // tile) so that the compiler can count them: the wait before a tile's MFMAs then leaves
+  // the next tile's loads in flight.
+  const int last_tile = w.key_begin + ((w.key_end - 1 - w.key_begin) & ~31);
+  auto clamp_tile = [&](int x) { return x < w.key_end ? x : last_tile; };
+  // The block of the tile after next is read one iteration early, so the next tile's
+  // loads issue as soon as an iteration starts.
   int t = w.key_begin + 32 * (split_keys ? wave : 0);
   Tile cur, nxt;
-  if (t < w.key_end) fetch(t, cur);
+  fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
+  uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
   for (; t < w.key_end; t += 32 * stride) {
-    const int tn = t + 32 * stride;
-    if (tn < w.key_end) fetch(tn, nxt);
+    const int tn = clamp_tile(t + 32 * stride);
+    fetch(tn, blk_next, nxt);
+    blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
+    // Issue the next tile's loads here, ahead of this tile's MFMAs.
+    __builtin_amdgcn_sched_barrier(0);
     floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {

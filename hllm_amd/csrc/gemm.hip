@@ -78,7 +78,11 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   half8 rbl[kLoB ? P : 1][kLoB ? NF : 1];
   const int first = kt0 + wk;
   const int steps = first < kt1 ? (kt1 - first + WK - 1) / WK : 0;
+  // Loads are unconditional so that the compiler can count them (a conditional load makes
+  // every wait drain the whole ring); k-steps past the range re-read the range's last one.
+  const int kt_last = max(0, min(kt1, KT) - 1);
   auto load = [&](int slot, int kt) {
+    kt = min(kt, kt_last);
 #pragma unroll
     for (int j = 0; j < NF; ++j) rb[slot][j] = W[j * frag_stride + (size_t)kt * 64];
 #pragma unroll
@@ -92,34 +96,42 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
       for (int j = 0; j < NF; ++j) rbl[slot][j] = WL[j * frag_stride + (size_t)kt * 64];
     }
   };
+  auto compute = [&](int s) {
 #pragma unroll
-  for (int s = 0; s < P; ++s)
-    if (s < steps) load(s, first + s * WK);
-  for (int base = 0; base < steps; base += P) {
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j) acc[i][j] = mfma(rb[s][j], rx[s][i], acc[i][j]);
+    if constexpr (kLoA) {
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j) acc2[i][j] = mfma(rb[s][j], rxl[s][i], acc2[i][j]);
+    }
+    if constexpr (kLoB) {
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j) acc2[i][j] = mfma(rbl[s][j], rx[s][i], acc2[i][j]);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < P; ++s) load(s, first + s * WK);
+  // Whole groups of P k-steps run branch-free, so each slot waits only for its own loads
+  // while the other P - 1 slots stay in flight; the last partial group follows.
+  int base = 0;
+  for (; base + P <= steps; base += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
-      const int step = base + s;
-      if (step < steps) {
-#pragma unroll
-        for (int i = 0; i < MF; ++i)
-#pragma unroll
-          for (int j = 0; j < NF; ++j) acc[i][j] = mfma(rb[s][j], rx[s][i], acc[i][j]);
-        if constexpr (kLoA) {
-#pragma unroll
-          for (int i = 0; i < MF; ++i)
-#pragma unroll
-            for (int j = 0; j < NF; ++j) acc2[i][j] = mfma(rb[s][j], rxl[s][i], acc2[i][j]);
-        }
-        if constexpr (kLoB) {
-#pragma unroll
-          for (int i = 0; i < MF; ++i)
-#pragma unroll
-            for (int j = 0; j < NF; ++j) acc2[i][j] = mfma(rbl[s][j], rx[s][i], acc2[i][j]);
-        }
-        if (step + P < steps) load(s, first + (step + P) * WK);
-      }
+      compute(s);
+      load(s, first + (base + s + P) * WK);
+      // Keep the slot's reload right after its MFMAs (the scheduler would otherwise sink
+      // every reload to the end of the group and leave nothing in flight).
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+#pragma unroll
+  for (int s = 0; s < P; ++s)
+    if (base + s < steps) compute(s);
 
   // Per-wave partial tiles -> one LDS tile, the K-interleaved waves adding in turn
   // (fixed order, so the sum is deterministic).
@@ -294,7 +306,10 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
 
   half8 rb[P][NFW];
   half8 rbl[kLoB ? P : 1][kLoB ? NFW : 1];
+  // Unconditional weight loads (see gemm_kernel); past the range they re-read the last k-step.
+  const int kt_last = max(0, min(kt1, KT) - 1);
   auto load_w = [&](int slot, int kt) {
+    kt = min(kt, kt_last);
 #pragma unroll
     for (int j = 0; j < NFW; ++j) rb[slot][j] = W[j * frag_stride + (size_t)kt * 64];
     if constexpr (kLoB) {
@@ -303,8 +318,7 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
     }
   };
 #pragma unroll
-  for (int sl = 0; sl < P; ++sl)
-    if (sl < steps) load_w(sl, kt0 + sl);
+  for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
   if (chunks > 0) {
     fetch_x(0);
     store_x(0);
@@ -316,8 +330,8 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
       const int step = c * KC + j;
+      const int slot = j % P;  // P divides KC, so step % P == j % P
       if (step < steps) {
-        const int slot = j % P;  // P divides KC, so step % P == j % P
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
           const half8 x = xb[(i * KC + j) * 64 + lane];
@@ -333,8 +347,9 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
             for (int n = 0; n < NFW; ++n) acc2[i][n] = mfma(rbl[slot][n], x, acc2[i][n]);
           }
         }
-        if (step + P < steps) load_w(slot, kt0 + step + P);
       }
+      load_w(slot, kt0 + step + P);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (c + 1 < chunks) store_x((c + 1) & 1);
     __syncthreads();
@@ -650,12 +665,38 @@ void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int 
   }
 }
 
-int gemm_default_config(int rows_bound) {
-  if (rows_bound <= 16) return 0;
-  if (rows_bound <= 32) return 1;
-  if (rows_bound <= 64) return 2;
-  return 3;
+namespace {
+
+struct Choice {
+  int config;
+  int ksplit;  // 0: the configuration's own rule
+};
+
+// Projection configuration by pass rows and shape, from sweeps of the Qwen3 projection
+// shapes on MI355X with weights streamed from HBM:
+//  - up to 64 rows: the register-streaming decode kernels (BM 16/32/64), except for very
+//    wide outputs (gate+up, LM head) with more than 32 rows, where staging the activations
+//    in LDS once per 256-feature tile wins;
+//  - more rows: the activation-staged kernel, BM 64 (BM 128 for wide outputs from 192
+//    rows). K is split only while there are few output tiles: about 200 workgroups are
+//    enough to stream the weights, and every split adds a partial tile round trip.
+Choice gemm_choice(int rows, int n, uint64_t kp) {
+  const bool wide = n >= 16384;
+  if (rows <= 64 && (!wide || rows <= 32)) return {rows <= 16 ? 0 : rows <= 32 ? 1 : 2, 0};
+  const int bm = wide && rows >= 192 ? 128 : 64;
+  const int config = bm == 128 ? 9 : 12;
+  const int kc = bm == 128 ? 4 : 8;
+  const long tiles = (long)((n + 255) / 256) * ((rows + bm - 1) / bm);
+  int ks = 1;
+  if (tiles < 150) {
+    const double want = 200.0 / (double)tiles;
+    while (ks * 2 <= want * 1.5 && ks < 16) ks *= 2;  // nearest power of two
+  }
+  const int cap = std::max(1, (int)(kp >> 5) / (2 * kc));
+  return {config, std::min(ks, cap)};
 }
+
+}  // namespace
 
 void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
   if (rows_bound <= 0) return;
@@ -663,9 +704,9 @@ void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bo
     const char* v = std::getenv("HLLM_ROCM_GEMM_CONFIG");
     return v ? std::atoi(v) : -1;
   }();
-  int config = gemm_default_config(rows_bound);
-  if (forced >= 0 && (rows_bound <= 64) == (forced != 3)) config = forced;
-  launch_gemm_config(stream, args, prec, rows_bound, cus, config, 0);
+  Choice c = gemm_choice(rows_bound, args.N, args.Kp);
+  if (forced >= 0) c = {forced, 0};
+  launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }
 
 }  // namespace hllm_rocm

@@ -31,11 +31,12 @@ struct AttnWork {
 // at least one row.
 __host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ? 1 : 64 / group; }
 
-// Splits of a block's `keys` key positions, every 1024 keys (shorter serial chains per
-// workgroup); splits are 32-key aligned and non-empty.
+// Splits of a block's `keys` key positions, 32-key aligned and non-empty: every 256 keys
+// for decode-like blocks (at most 16 query vectors: the workgroup's four waves share the
+// keys, and short splits balance rows of very different context lengths), every 1024 keys
+// for prefill blocks (fewer partial results to combine).
 __host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits) {
-  (void)vectors;
-  const int unit = 1024;
+  const int unit = vectors <= 16 ? 256 : 1024;
   int splits = (keys + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = ((keys + splits - 1) / splits + 31) & ~31;
