@@ -369,10 +369,15 @@ __global__ void __launch_bounds__(kThreads) attention_valu_kernel(AttentionArgs 
 
 // ---------------------------------------------------------------- split combine
 
-// One block per (row, query head): merge the row's splits, normalise, write the operand.
-// MFMA-path rows with a single split were written by the attention kernel already.
-__global__ void attention_combine_kernel(AttentionArgs a, int mfma_path) {
-  const int r = blockIdx.x, qh = blockIdx.y;
+// One wave per (row, query head), four per block: merge the row's splits, normalise and
+// write the operand. Lane s < splits holds split s's statistics; lane L owns head
+// dimensions L*E .. L*E+E-1 (E = D / 64, at least 1). MFMA-path rows with a single split
+// were written by the attention kernel already.
+__global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a, int mfma_path) {
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (pair >= a.rows * a.q_heads) return;
+  const int r = pair / a.q_heads, qh = pair - r * a.q_heads;
   const int D = a.head_dim;
   int splits;
   if (mfma_path) {
@@ -385,24 +390,36 @@ __global__ void attention_combine_kernel(AttentionArgs a, int mfma_path) {
   }
   const int stride = D + 2;
   const float* part = partial_at(a, r, qh, 0);
-  float m = -INFINITY;
-  for (int s = 0; s < splits; ++s) m = fmaxf(m, part[s * stride + D]);
+  const float ms = lane < splits ? part[lane * stride + D] : -INFINITY;
+  const float ls = lane < splits ? part[lane * stride + D + 1] : 0.0f;
+  float m = ms;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
   const float ref = m == -INFINITY ? 0.0f : m;
-  float total = 0.0f;
-  for (int s = 0; s < splits; ++s) total += part[s * stride + D + 1] * rescale(part[s * stride + D], ref);
+  const float ws = lane < splits ? rescale(ms, ref) : 0.0f;
+  float total = ls * ws;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o, 64);
   const float inv = 1.0f / total;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float v = 0.0f;
-    for (int s = 0; s < splits; ++s) v += part[s * stride + d] * rescale(part[s * stride + D], ref);
-    const float y = v * inv;
-    const uint64_t at = flayout_index(r, (uint64_t)qh * D + d, a.out_cols_padded);
-    const _Float16 hi = to_half(y);
-    a.out_hi[at] = __builtin_bit_cast(uint16_t, hi);
-    if (a.out_lo) a.out_lo[at] = __builtin_bit_cast(uint16_t, to_half((y - (float)hi) * kLoScale));
+  const int E = D >= 64 ? D / 64 : 1;
+  if (lane * E < D) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; ++sp) {
+      const float w = __shfl(ws, sp, 64);
+      const float* src = part + (size_t)sp * stride + lane * E;
+      for (int e = 0; e < E; ++e) v[e] += src[e] * w;
+    }
+    for (int e = 0; e < E; ++e) {
+      const float y = v[e] * inv;
+      const uint64_t at = flayout_index(r, (uint64_t)qh * D + lane * E + e, a.out_cols_padded);
+      const _Float16 hi = to_half(y);
+      a.out_hi[at] = __builtin_bit_cast(uint16_t, hi);
+      if (a.out_lo) a.out_lo[at] = __builtin_bit_cast(uint16_t, to_half((y - (float)hi) * kLoScale));
+    }
   }
   // Zero the operand's padded columns (their weights are zero; the values must be finite).
   if (qh == 0) {
-    for (uint64_t c = (uint64_t)a.q_heads * D + threadIdx.x; c < a.out_cols_padded; c += blockDim.x) {
+    for (uint64_t c = (uint64_t)a.q_heads * D + lane; c < a.out_cols_padded; c += 64) {
       const uint64_t at = flayout_index(r, c, a.out_cols_padded);
       a.out_hi[at] = 0;
       if (a.out_lo) a.out_lo[at] = 0;
@@ -446,7 +463,9 @@ void launch_attention(hipStream_t stream, const AttentionArgs& a) {
     else
       observed("attention_valu_kernel<_Float16>", [&] { attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a); });
   }
-  observed("attention_combine_kernel", [&] { attention_combine_kernel<<<dim3(a.rows, a.q_heads), 128, 0, stream>>>(a, mfma_path ? 1 : 0); });
+  const unsigned pairs = (unsigned)(a.rows * a.q_heads);
+  observed("attention_combine_kernel",
+           [&] { attention_combine_kernel<<<(pairs + 3) / 4, 256, 0, stream>>>(a, mfma_path ? 1 : 0); });
 }
 
 }  // namespace hllm_rocm

@@ -167,6 +167,17 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
     __syncthreads();
   }
 
+  if (a.ksplit > 1 && a.defer_reduce) {
+    // Partial output of this K split as a row-major [M][N] matrix of its own; the consumer
+    // of the projection sums the splits in order.
+    float* ws = a.workspace + (size_t)split * a.M * a.N;
+    for (int e = threadIdx.x; e < BM * BN; e += NT) {
+      const int m = e / BN, n = e % BN;
+      const int row = tile_m * BM + m, col = tile_n * BN + n;
+      if (row < M && col < a.N) ws[(size_t)row * a.N + col] = lds[m * LDT + n];
+    }
+    return;
+  }
   if (a.ksplit > 1) {
     // Partial tile of this K split; gemm_reduce_kernel sums the splits in order and applies
     // the epilogue after this kernel completes (no device-scope fences needed).
@@ -368,6 +379,30 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
     return v;
   };
   const int q4 = (lane >> 4) * 4, t16 = lane & 15;
+  const bool vec = (a.N & 3) == 0 && (a.ldo & 3) == 0;
+  if (a.ksplit > 1 && a.defer_reduce) {
+    // Partial output of this K split as a row-major [M][N] matrix (see gemm_kernel).
+    float* ws = a.workspace + (size_t)split * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const int row = tile_m * BM + i * 16 + t16;
+      if (row >= M) continue;
+#pragma unroll
+      for (int n = 0; n < NFW; ++n) {
+        const int col = tile_n * BN + (wave * NFW + n) * 16 + q4;
+        const floatx4 v = value(i, n);
+        float* dst = ws + (size_t)row * a.N + col;
+        if (vec && col + 3 < a.N) {
+          *reinterpret_cast<floatx4*>(dst) = v;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (col + t < a.N) dst[t] = v[t];
+        }
+      }
+    }
+    return;
+  }
   if (a.ksplit > 1) {
     // Partial tile of this K split, summed in split order by gemm_reduce_kernel.
     float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
@@ -410,7 +445,6 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
     }
     return;
   }
-  const bool vec = (a.ldo & 3) == 0;
 #pragma unroll
   for (int i = 0; i < MF; ++i) {
     const int row = m_base + i * 16 + t16;
@@ -531,9 +565,16 @@ void run(dim3 grid, int threads, size_t lds, hipStream_t stream, const GemmArgs&
                                                                            tiles_padded); });
 }
 
+// Fits the K split to the workspace: tile partials for the reduce kernel, or whole partial
+// output matrices when the consumer sums them.
+int fit_ksplit(const GemmArgs& a, int ksplit, size_t tiles, size_t tile_floats) {
+  const size_t need = a.defer_reduce ? (size_t)a.M * a.N : tiles * tile_floats;
+  return (size_t)ksplit * need > a.workspace_floats ? 1 : ksplit;
+}
+
 template <int MF, int NF, int WM, int WN, int WK, int P>
-void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
-                   int min_k_per_wave, int forced_ksplit) {
+int launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
+                  int min_k_per_wave, int forced_ksplit) {
   constexpr int BM = 16 * MF * WM, BN = 16 * NF * WN, NT = 64 * WM * WN * WK;
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
@@ -548,7 +589,7 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
   }
   ksplit = std::min(ksplit, std::max(1, KT / (WK * min_k_per_wave)));
   const int tiles_padded = (tiles + kXcds - 1) / kXcds * kXcds;
-  if ((size_t)tiles * ksplit * BM * BN > a.workspace_floats) ksplit = 1;
+  ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
   a.ksplit = ksplit;
   const size_t lds = ((size_t)BM * (BN + 4) + 4) * sizeof(float);
   dim3 grid(tiles_padded * ksplit, 1, 1);
@@ -563,14 +604,16 @@ void launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int
       run<MF, NF, WM, WN, WK, P, kSplitAB>(grid, NT, lds, stream, a, n_tiles, tiles, tiles_padded);
       break;
   }
+  if (ksplit > 1 && a.defer_reduce) return ksplit;
   if (ksplit > 1) {
     const int64_t threads = (int64_t)tiles * BM * BN / 8;
     observed(kernel_name<BM, BN>("gemm_reduce_kernel"), [&] { gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles); });
   }
+  return 0;
 }
 
 template <int MF, int NFW, int KC, int P>
-void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
+int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
                  int forced_ksplit) {
   constexpr int BM = 16 * MF, BN = 64 * NFW;
   const int n_tiles = (a.N + BN - 1) / BN;
@@ -581,7 +624,7 @@ void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int t
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
   int ksplit = forced_ksplit > 0 ? forced_ksplit : (tiles < target_ctas ? (target_ctas + tiles - 1) / tiles : 1);
   ksplit = std::min(ksplit, std::max(1, KT / (2 * KC)));
-  if ((size_t)tiles * ksplit * BM * BN > a.workspace_floats) ksplit = 1;
+  ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
   a.ksplit = ksplit;
   const int xp = prec >= kSplitA ? 2 : 1;
   const size_t lds = (size_t)2 * MF * KC * 64 * xp * 16;
@@ -606,10 +649,12 @@ void launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int t
       go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>, kernel_name<MF, NFW, KC, P, kSplitAB>("gemm_xlds_kernel"));
       break;
   }
+  if (ksplit > 1 && a.defer_reduce) return ksplit;
   if (ksplit > 1) {
     const int64_t threads = (int64_t)tiles * BM * BN / 8;
     observed(kernel_name<BM, BN>("gemm_reduce_kernel"), [&] { gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles); });
   }
+  return 0;
 }
 
 }  // namespace
@@ -620,47 +665,47 @@ int gemm_tile_rows(int rows_bound) { return rows_bound <= 64 ? 64 : 128; }
 //   0..2: decode, BM = 16/32/64, BN = 64, four K-waves, ring of 4 k-steps
 //   3:    prefill, 128 x 128, 2 x 2 waves, ring of 2 k-steps
 //   4..6: decode, BM = 16/32/64, BN = 128 (NF = 8), two K-waves, ring of 4
-void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
+int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
                         int config, int forced_ksplit) {
   switch (config) {
     case 0:
-      launch_config<1, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
+      return launch_config<1, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 1:
-      launch_config<2, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
+      return launch_config<2, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 2:
-      launch_config<4, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
+      return launch_config<4, 4, 1, 1, 4, 4>(stream, args, prec, rows_bound, cus * 5 / 8, 2, forced_ksplit);
       break;
     case 4:
-      launch_config<1, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      return launch_config<1, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
       break;
     case 5:
-      launch_config<2, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      return launch_config<2, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
       break;
     case 6:
-      launch_config<4, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
+      return launch_config<4, 8, 1, 1, 2, 4>(stream, args, prec, rows_bound, 2 * cus, 2, forced_ksplit);
       break;
     case 7:  // activation-staged: BM 64 x BN 256
-      launch_xlds<4, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<4, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     case 8:  // BM 128 x BN 256, chunks of 2 k-steps, ring of 2
-      launch_xlds<8, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<8, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     case 9:  // BM 128 x BN 256, chunks of 4, ring of 2
-      launch_xlds<8, 4, 4, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<8, 4, 4, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     case 10:  // BM 128 x BN 256, chunks of 4, ring of 4
-      launch_xlds<8, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<8, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     case 11:  // BM 32 x BN 256
-      launch_xlds<2, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<2, 4, 4, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     case 12:  // BM 64 x BN 256, chunks of 8, ring of 4
-      launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+      return launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
     default:
-      launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
+      return launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
       break;
   }
 }
@@ -698,15 +743,15 @@ Choice gemm_choice(int rows, int n, uint64_t kp) {
 
 }  // namespace
 
-void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
-  if (rows_bound <= 0) return;
+int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
+  if (rows_bound <= 0) return 0;
   static const int forced = [] {
     const char* v = std::getenv("HLLM_ROCM_GEMM_CONFIG");
     return v ? std::atoi(v) : -1;
   }();
   Choice c = gemm_choice(rows_bound, args.N, args.Kp);
   if (forced >= 0) c = {forced, 0};
-  launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
+  return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }
 
 }  // namespace hllm_rocm

@@ -26,6 +26,7 @@ struct GemmArgs {
   size_t workspace_floats;
   int32_t* counters;           // per-tile arrival counters, zero between launches
   int counter_count;
+  int defer_reduce;            // leave K-split partials as [split][M][N] for the consumer
   int epilogue;
   float* out;                  // kEpiStore / kEpiResidual
   int ldo;
@@ -36,9 +37,11 @@ struct GemmArgs {
 
 // Rows of the tile a launch with `rows_bound` rows uses (activation buffers are padded to it).
 int gemm_tile_rows(int rows_bound);
-void launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus);
+// Returns 0 when the epilogue has been applied, or (defer_reduce only) the number of K-split
+// partial output matrices left in the workspace for the consumer to sum in order.
+int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus);
 // An explicit configuration of the table in gemm.hip (tuning), optionally forcing the K split.
-void launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
+int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
                         int config, int forced_ksplit);
 
 }  // namespace hllm_rocm

@@ -107,19 +107,31 @@ void launch_boundary_decode(hipStream_t stream, const uint16_t* in, int rows, in
 void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hidden, uint16_t* out,
                             int32_t* flags);
 
+// K-split partial outputs a projection left for its consumer: `parts` row-major matrices
+// of the consumer's row width, `stride` floats apart, summed in order (0 = none).
+struct Partials {
+  const float* data = nullptr;
+  int parts = 0;
+  uint64_t stride = 0;
+};
+
 // y = (x * inv_rms) * w written to F-layout hi (+ lo when lo != nullptr); rows may be
 // gathered through `row_index` (nullptr = identity) with `count` read from device
-// memory when `device_rows` is non-null.
-void launch_rmsnorm_flayout(hipStream_t stream, const float* h, int hidden, const int32_t* row_index,
+// memory when `device_rows` is non-null. With `residual` partials (identity rows only)
+// the row is first updated in place: h += sum of the partials.
+void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int32_t* row_index,
                             int rows, const int32_t* device_rows, const float* weight, float eps,
-                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded);
+                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
+                            Partials residual = {});
 
 // Per-head QK-norm (optional) + rotate-half RoPE from tables + paged KV append. `qkv` is
 // [rows][(Q + 2K) * D] F32; q goes to `q_out` [rows][Q * D] F32.
+// With `qkv_parts`, the projection is the sum of its K-split partials instead of `qkv`.
 void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
                             int head_dim, const float* q_norm, const float* k_norm, float eps,
                             const float* rope_cos, const float* rope_sin, const int32_t* row_position,
-                            const int32_t* row_slot, KvView kv, int layer, float* q_out);
+                            const int32_t* row_slot, KvView kv, int layer, float* q_out,
+                            Partials qkv_parts = {});
 
 // Split-context GQA attention for every packed row against its sequence's paged cache
 // (positions 0..row_position), then the split combine into F-layout A operands.

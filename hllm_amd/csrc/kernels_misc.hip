@@ -143,29 +143,55 @@ __global__ void boundary_encode_kernel(const float* h, uint64_t n, uint16_t* out
 // One block per row; each thread keeps its 8-column chunks in registers between the
 // square sum and the scaled store (hidden sizes up to 256 * 8 * kNormChunks).
 constexpr int kNormChunks = 4;
+__device__ inline void load8(const float* x, int c0, int hidden, bool vec, float* v) {
+  if (vec && c0 < hidden) {
+    const floatx4 a = *reinterpret_cast<const floatx4*>(x + c0);
+    const floatx4 b = *reinterpret_cast<const floatx4*>(x + c0 + 4);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+    v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c0 + j < hidden ? x[c0 + j] : 0.0f;
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) rmsnorm_flayout_kernel(
-    const float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
-    const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
+    float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
+    const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
+    Partials residual) {
   __shared__ float scratch[4];
   const int r = blockIdx.x;
   const int count = device_rows ? *device_rows : rows;
   if (r >= count) return;
   const int src = row_index ? row_index[r] : r;
-  const float* x = h + (size_t)src * hidden;
+  float* x = h + (size_t)src * hidden;
   float v[kNormChunks][8];
   float squares = 0.0f;
   const bool vec = (hidden & 7) == 0;
 #pragma unroll
   for (int q = 0; q < kNormChunks; ++q) {
     const int c0 = (threadIdx.x + q * blockDim.x) * 8;
-    if (vec && c0 < hidden) {
-      const floatx4 a = *reinterpret_cast<const floatx4*>(x + c0);
-      const floatx4 b = *reinterpret_cast<const floatx4*>(x + c0 + 4);
-      v[q][0] = a[0]; v[q][1] = a[1]; v[q][2] = a[2]; v[q][3] = a[3];
-      v[q][4] = b[0]; v[q][5] = b[1]; v[q][6] = b[2]; v[q][7] = b[3];
-    } else {
+    load8(x, c0, hidden, vec, v[q]);
+    if (residual.parts > 0 && c0 < hidden) {
+      // The projection's K-split partials summed in split order, then the residual add
+      // (the order of the reduce kernel's residual epilogue), written back in place.
+      float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < residual.parts; ++s) {
+        float p[8];
+        load8(residual.data + s * residual.stride + (size_t)src * hidden, c0, hidden, vec, p);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[q][j] = c0 + j < hidden ? x[c0 + j] : 0.0f;
+        for (int j = 0; j < 8; ++j) y[j] += p[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[q][j] += y[j];
+      if (vec) {
+        *reinterpret_cast<floatx4*>(x + c0) = floatx4{v[q][0], v[q][1], v[q][2], v[q][3]};
+        *reinterpret_cast<floatx4*>(x + c0 + 4) = floatx4{v[q][4], v[q][5], v[q][6], v[q][7]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (c0 + j < hidden) x[c0 + j] = v[q][j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) squares += v[q][j] * v[q][j];
@@ -206,7 +232,8 @@ __device__ inline uint64_t kv_index(const KvView& kv, int layer, int slot, int w
 __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
     const float* qkv, int q_heads, int kv_heads, int head_dim, const float* q_norm,
     const float* k_norm, float eps, const float* rope_cos, const float* rope_sin,
-    const int32_t* row_position, const int32_t* row_slot, KvView kv, int layer, float* q_out) {
+    const int32_t* row_position, const int32_t* row_slot, KvView kv, int layer, float* q_out,
+    Partials parts) {
   const int r = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
   const int heads = q_heads + 2 * kv_heads;
@@ -227,7 +254,20 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d = lane + 64 * j;
-      v[j] = (j < per_lane && d < D) ? src[d] : 0.0f;
+      if (j < per_lane && d < D) {
+        if (parts.parts > 0) {
+          // K-split partials of the projection, summed in split order from zero (the
+          // reduce kernel's order for a plain store).
+          const size_t at = (size_t)r * heads * D + (size_t)head * D + d;
+          float y = 0.0f;
+          for (int s = 0; s < parts.parts; ++s) y += parts.data[s * parts.stride + at];
+          v[j] = y;
+        } else {
+          v[j] = src[d];
+        }
+      } else {
+        v[j] = 0.0f;
+      }
       squares += v[j] * v[j];
     }
     if (!is_v) {
@@ -477,22 +517,24 @@ void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hi
                                                                                       flags); });
 }
 
-void launch_rmsnorm_flayout(hipStream_t stream, const float* h, int hidden, const int32_t* row_index,
+void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int32_t* row_index,
                             int rows, const int32_t* device_rows, const float* weight, float eps,
-                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded) {
+                            uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
+                            Partials residual) {
   if (rows <= 0) return;
   observed("rmsnorm_flayout_kernel", [&] { rmsnorm_flayout_kernel<<<rows, kBlock, 0, stream>>>(h, hidden, row_index, rows, device_rows,
-                                                      weight, eps, out_hi, out_lo, cols_padded); });
+                                                      weight, eps, out_hi, out_lo, cols_padded, residual); });
 }
 
 void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
                             int head_dim, const float* q_norm, const float* k_norm, float eps,
                             const float* rope_cos, const float* rope_sin, const int32_t* row_position,
-                            const int32_t* row_slot, KvView kv, int layer, float* q_out) {
+                            const int32_t* row_slot, KvView kv, int layer, float* q_out,
+                            Partials qkv_parts) {
   const int heads = q_heads + 2 * kv_heads;
   observed("qkv_rope_append_kernel", [&] { qkv_rope_append_kernel<<<dim3(rows, (heads + 3) / 4), kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
                                                       k_norm, eps, rope_cos, rope_sin, row_position,
-                                                      row_slot, kv, layer, q_out); });
+                                                      row_slot, kv, layer, q_out, qkv_parts); });
 }
 
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,

@@ -145,9 +145,10 @@ class Stage {
                 uint64_t seed, uint64_t tensor_id, float mean, float sigma, uint64_t row_base,
                 uint64_t rows);
   void read_flags(const char* context);
-  void gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo, int rows,
+  int gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo, int rows,
             int n, int epilogue, float* out, int ldo, uint16_t* out_hi, uint16_t* out_lo,
-            uint64_t out_cols_padded);
+            uint64_t out_cols_padded,
+           bool defer = false);
   template <typename F>
   void timed(const char* family, uint64_t bytes, double flops, F&& launch);
   hipEvent_t take_event();
@@ -866,10 +867,13 @@ std::string Stage::profile_records() {
 
 // --------------------------------------------------------------------- the pass
 
-void Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo,
-                 int rows, int n, int epilogue, float* out, int ldo, uint16_t* out_hi,
-                 uint16_t* out_lo, uint64_t out_cols_padded) {
+// Launches one projection; with `defer`, K-split partials are left in the workspace for the
+// consumer and their count is returned (0: the epilogue has been applied).
+int Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo,
+                int rows, int n, int epilogue, float* out, int ldo, uint16_t* out_hi,
+                uint16_t* out_lo, uint64_t out_cols_padded, bool defer) {
   GemmArgs a{};
+  a.defer_reduce = defer ? 1 : 0;
   a.w_hi = w.hi.as<uint16_t>();
   a.w_lo = w.lo.as<uint16_t>();
   a.x_hi = x_hi;
@@ -893,7 +897,9 @@ void Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, cons
   const uint64_t obytes = epilogue == kEpiSwiglu ? (uint64_t)rows * (n / 2) * 2 * (out_lo ? 2 : 1)
                                                  : (uint64_t)rows * n * 4 * (epilogue == kEpiResidual ? 2 : 1);
   const double flops = 2.0 * rows * n * w.cols;
-  timed(family, wbytes + xbytes + obytes, flops, [&] { launch_gemm(stream_, a, prec_, rows, cus_); });
+  int parts = 0;
+  timed(family, wbytes + xbytes + obytes, flops, [&] { parts = launch_gemm(stream_, a, prec_, rows, cus_); });
+  return parts;
 }
 
 void Stage::fail_pass(const std::vector<uint32_t>& sequences) {
@@ -1021,21 +1027,27 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     const float eps = c_.rms_norm_epsilon;
     const uint64_t a1_cols = std::max(QDp_, Ip_);
     (void)a1_cols;
+    // K-split partials of a projection are summed by the kernel that consumes it: q/k/v's
+    // by RoPE/append, o's and down's (residual adds) by the next RMSNorm. `pending` holds
+    // the previous layer's down-projection partials until this layer's input norm.
+    float* ws = gemm_ws_.as<float>();
+    Partials pending{};
     for (uint64_t l = 0; l < L_; ++l) {
       if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
       Layer& w = *layers_[l];
       timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.input_norm.as<float>(), eps, a0h, a0l,
-                               Hp_);
+                               Hp_, pending);
       });
-      gemm("gemm_qkv", w.qkv, a0h, a0l, R, (int)qkv_n_, kEpiStore, qkv_.as<float>(), (int)qkv_n_, nullptr,
-           nullptr, 0);
+      pending = {};
+      const int qkv_parts = gemm("gemm_qkv", w.qkv, a0h, a0l, R, (int)qkv_n_, kEpiStore, qkv_.as<float>(),
+                                 (int)qkv_n_, nullptr, nullptr, 0, true);
       timed("rope_append", (uint64_t)R * qkv_n_ * 6, 0.0, [&] {
         launch_qkv_rope_append(stream_, qkv_.as<float>(), R, (int)Q_, (int)K_, (int)D_,
                                c_.query_key_norm ? w.q_norm.as<float>() : nullptr,
                                c_.query_key_norm ? w.k_norm.as<float>() : nullptr, eps, rope_cos_.as<float>(),
                                rope_sin_.as<float>(), pack_.row_position, pack_.row_slot, kv_, (int)l,
-                               q_.as<float>());
+                               q_.as<float>(), Partials{ws, qkv_parts, (uint64_t)R * qkv_n_});
       });
       AttentionArgs at{};
       at.work = attn_work_.as<AttnWork>();
@@ -1061,13 +1073,19 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       at.out_lo = a1l;
       at.out_cols_padded = QDp_;
       timed("attention", attn_bytes, attn_flops, [&] { launch_attention(stream_, at); });
-      gemm("gemm_o", w.o, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0);
+      const int o_parts = gemm("gemm_o", w.o, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0,
+                               true);
       timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.post_norm.as<float>(), eps, a0h, a0l,
-                               Hp_);
+                               Hp_, Partials{ws, o_parts, (uint64_t)R * H_});
       });
       gemm("gemm_gate_up", w.gate_up, a0h, a0l, R, (int)(2 * Ip_), kEpiSwiglu, nullptr, 0, a1h, a1l, Ip_);
-      gemm("gemm_down", w.down, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr, nullptr, 0);
+      // The last layer's residual completes here (the final norm gathers sampled rows, and
+      // the boundary and trace read the whole stream).
+      const bool defer_down = l + 1 < L_ && !pass.trace_hidden;
+      const int down_parts = gemm("gemm_down", w.down, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr,
+                                  nullptr, 0, defer_down);
+      pending = Partials{ws, down_parts, (uint64_t)R * H_};
       HIP_CHECK(hipGetLastError());
       if (pass.trace_hidden) {
         HIP_CHECK(hipMemcpyAsync(pass.trace_hidden + l * (size_t)R * H_, h, (size_t)R * H_ * sizeof(float),
