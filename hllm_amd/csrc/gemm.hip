@@ -722,22 +722,33 @@ struct Choice {
 //  - up to 64 rows: the register-streaming decode kernels (BM 16/32/64), except for very
 //    wide outputs (gate+up, LM head) with more than 32 rows, where staging the activations
 //    in LDS once per 256-feature tile wins;
-//  - more rows: the activation-staged kernel, BM 64 (BM 128 for wide outputs from 192
-//    rows). K is split only while there are few output tiles: about 200 workgroups are
-//    enough to stream the weights, and every split adds a partial tile round trip.
-Choice gemm_choice(int rows, int n, uint64_t kp) {
+//  - more rows: the activation-staged kernel, BM 64, or BM 128 from 384 rows (and for
+//    wide outputs from 192 rows).
+// K is split while there are few output tiles. When the consumer sums the partials
+// (`deferred`) a split costs one partial write, so about 220-280 workgroups are targeted;
+// otherwise a reduce kernel reads every partial back, so splits stop at about 200
+// workgroups, in powers of two.
+Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred) {
   const bool wide = n >= 16384;
-  if (rows <= 64 && (!wide || rows <= 32)) return {rows <= 16 ? 0 : rows <= 32 ? 1 : 2, 0};
-  const int bm = wide && rows >= 192 ? 128 : 64;
+  const auto rounded = [](double x) { return std::max(1, (int)(x + 0.5)); };
+  if (rows <= 64 && (!wide || rows <= 32)) {
+    const int config = rows <= 16 ? 0 : rows <= 32 ? 1 : 2;
+    const int tiles = (n + 63) / 64;
+    const int cap = std::max(1, (int)(kp >> 5) / 8);  // at least two k-steps per K-wave
+    return {config, deferred ? std::min(rounded(220.0 / tiles), cap) : 0};
+  }
+  const int bm = rows >= 384 || (wide && rows >= 192) ? 128 : 64;
   const int config = bm == 128 ? 9 : 12;
   const int kc = bm == 128 ? 4 : 8;
   const long tiles = (long)((n + 255) / 256) * ((rows + bm - 1) / bm);
+  const int cap = std::max(1, (int)(kp >> 5) / (2 * kc));
   int ks = 1;
-  if (tiles < 150) {
+  if (deferred) {
+    ks = std::min(rounded(280.0 / (double)tiles), 8);
+  } else if (tiles < 150) {
     const double want = 200.0 / (double)tiles;
     while (ks * 2 <= want * 1.5 && ks < 16) ks *= 2;  // nearest power of two
   }
-  const int cap = std::max(1, (int)(kp >> 5) / (2 * kc));
   return {config, std::min(ks, cap)};
 }
 
@@ -749,7 +760,7 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
     const char* v = std::getenv("HLLM_ROCM_GEMM_CONFIG");
     return v ? std::atoi(v) : -1;
   }();
-  Choice c = gemm_choice(rows_bound, args.N, args.Kp);
+  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0);
   if (forced >= 0) c = {forced, 0};
   return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }

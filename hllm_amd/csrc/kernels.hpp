@@ -31,25 +31,25 @@ struct AttnWork {
 // at least one row.
 __host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ? 1 : 64 / group; }
 
-// Splits of a block's `keys` key positions, 32-key aligned and non-empty: every 256 keys
-// for decode-like blocks (at most 16 query vectors: the workgroup's four waves share the
+// Splits of a block's `keys` key positions, 32-key aligned and non-empty: every
+// `decode_unit` keys (a multiple of 32; 256 by default) for decode-like blocks (at most 16 query vectors: the workgroup's four waves share the
 // keys, and short splits balance rows of very different context lengths), every 1024 keys
 // for prefill blocks (fewer partial results to combine).
-__host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits) {
-  const int unit = vectors <= 16 ? 256 : 1024;
+__host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits, int decode_unit) {
+  const int unit = vectors <= 16 ? decode_unit : 1024;
   int splits = (keys + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = ((keys + splits - 1) / splits + 31) & ~31;
   return per;
 }
 __host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
-                                              int max_splits) {
+                                              int max_splits, int decode_unit) {
   const int qb = attn_block_rows(group);
   int work = 0;
   for (int r0 = 0; r0 < query_tokens; r0 += qb) {
     const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
     const int keys = first_position + r0 + rows;
-    const int per = attn_split_keys(keys, rows * group, max_splits);
+    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
     work += (keys + per - 1) / per;
   }
   return work;
@@ -69,6 +69,7 @@ struct PackOut {
   int32_t* row_splits;     // [rows] key splits of the row's attention block
   int attn_group;          // query heads per KV head
   int attn_max_splits;
+  int attn_decode_unit;    // keys per split of decode-like blocks (attn_split_keys)
 };
 
 // Paged KV pool: [layers][blocks][K, V][kv_heads][...] with keys as [block_tokens][head_dim]

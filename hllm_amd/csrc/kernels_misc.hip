@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
     if (out.attn_work)
       work += attn_item_work((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
-                             out.attn_max_splits);
+                             out.attn_max_splits, out.attn_decode_unit);
   }
   offset = wave_sum_int(offset);
   samples = wave_sum_int(samples);
@@ -93,7 +93,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     for (int r0 = 0; r0 < q; r0 += qb) {
       const int rows = min(qb, q - r0);
       const int keys = first + r0 + rows;
-      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits);
+      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
       const int splits = (keys + per - 1) / per;
       for (int s = 0; s < splits; ++s) {
         out.attn_work[work++] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per,

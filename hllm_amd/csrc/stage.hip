@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -383,6 +384,14 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     pack_.attn_work = attn_work_.as<AttnWork>();
     pack_.attn_group = (int)group;
     pack_.attn_max_splits = kMaxSplits;
+    // Keys per split of decode-like attention blocks; HLLM_ROCM_ATTN_DECODE_SPLIT overrides
+    // it for tuning (a multiple of 32).
+    pack_.attn_decode_unit = 256;
+    if (const char* v = std::getenv("HLLM_ROCM_ATTN_DECODE_SPLIT")) {
+      const int unit = std::atoi(v);
+      if (unit < 32 || unit % 32) fail(HLLM_INVALID_REQUEST, "HLLM_ROCM_ATTN_DECODE_SPLIT must be a multiple of 32");
+      pack_.attn_decode_unit = unit;
+    }
   }
   if (!c.first_stage || !c.final_stage) boundary_dev_.allocate(R * H_ * 2, "boundary");
   pin_items_.allocate(items_max_ * sizeof(ItemMeta));
@@ -991,7 +1000,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   if (mfma_attention_) {
     for (uint32_t i = 0; i < n; ++i)
       attn_work_count += attn_item_work((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
-                                        (int)(Q_ / K_), kMaxSplits);
+                                        (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit);
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
 
