@@ -19,6 +19,8 @@
 // accumulation are F32 (cpp/src/cpu/llama.cpp:67-112; cpp/src/cuda/stage.cpp:291-300).
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace hllm_rocm {
 namespace {
 
@@ -69,7 +71,8 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   const int my_pos = w.position0 + vr;
   const int seq = a.items[w.item].sequence;
   const int bt = a.kv.block_tokens, KVH = a.kv_heads;
-  if (!split_keys && vf * 16 >= nvec) return;  // no __syncthreads on this path
+  // Waves whose vectors lie past the block's end still stage K/V tiles and meet the
+  // barriers of the prefill path; their results are never written.
   // A tile's physical block: a wave-uniform table entry, read through the scalar cache so
   // that waiting for it never drains the vector loads of the tile in flight. Tiles are
   // 32-key aligned and blocks a multiple of 32 keys, so a tile lies in one block.
@@ -99,8 +102,7 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
   for (int df = 0; df < DF; ++df) o[df] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  const int stride = split_keys ? 4 : 1;
-  // K and V fragments of one 32-key tile; the next tile's are loaded while this one is used.
+  // K and V fragments of one 32-key tile.
   struct Tile {
     half8 k0[KK], k1[KK];
     half8 v[DF];
@@ -123,74 +125,144 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       f.v[df] = *reinterpret_cast<const half8*>(vb + (size_t)(16 * df + col) * 32 + 8 * quad);
     }
   };
-  // Loads are issued unconditionally (a tile past the range re-reads the range's last
-  // tile) so that the compiler can count them: the wait before a tile's MFMAs then leaves
-  // the next tile's loads in flight.
-  const int last_tile = w.key_begin + ((w.key_end - 1 - w.key_begin) & ~31);
-  auto clamp_tile = [&](int x) { return x < w.key_end ? x : last_tile; };
-  // The block of the tile after next is read one iteration early, so the next tile's
-  // loads issue as soon as an iteration starts.
-  int t = w.key_begin + 32 * (split_keys ? wave : 0);
-  Tile cur, nxt;
-  fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
-  uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
-  for (; t < w.key_end; t += 32 * stride) {
-    const int tn = clamp_tile(t + 32 * stride);
-    fetch(tn, blk_next, nxt);
-    blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
-    // Issue the next tile's loads here, ahead of this tile's MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
-    floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  // One tile's scores, online softmax update and value accumulation.
+  auto consume = [&](int t, const Tile& f) {
+  floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      s0 = mfma(cur.k0[kk], qf[kk], s0);
-      s1 = mfma(cur.k1[kk], qf[kk], s1);
+  for (int kk = 0; kk < KK; ++kk) {
+    s0 = mfma(f.k0[kk], qf[kk], s0);
+    s1 = mfma(f.k1[kk], qf[kk], s1);
+  }
+  float sc[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
+    sc[i] = (v_ok && p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
+    sc[4 + i] = (v_ok && p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+  }
+  float tmax = sc[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sc[i]);
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float m_new = fmaxf(m, tmax);
+  const float base = m_new == -INFINITY ? 0.0f : m_new;
+  const float alpha = rescale(m, base);
+  half8 pf;
+  float psum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = sc[i] == -INFINITY ? 0.0f : expf(sc[i] - base);
+    psum += p;
+    pf[i] = to_half(p);
+  }
+  psum += __shfl_xor(psum, 16, 64);
+  psum += __shfl_xor(psum, 32, 64);
+  l = l * alpha + psum;
+  m = m_new;
+  // A tile that runs past the key range reads cache slots no pass has written: zero
+  // them, since a zero probability does not cancel a non-finite value.
+  const bool tail = t + 32 > w.key_end;
+#pragma unroll
+  for (int df = 0; df < DF; ++df) {
+    o[df][0] *= alpha;
+    o[df][1] *= alpha;
+    o[df][2] *= alpha;
+    o[df][3] *= alpha;
+    half8 av = f.v[df];
+    if (tail) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (t + 8 * quad + j >= w.key_end) av[j] = (_Float16)0.0f;
     }
-    float sc[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
-      sc[i] = (v_ok && p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
-      sc[4 + i] = (v_ok && p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+    o[df] = mfma(av, pf, o[df]);
+  }
+  };
+
+  if (split_keys) {
+    // Decode-like blocks: the four waves take interleaved tiles, each loading its own
+    // fragments from HBM straight into registers, one tile ahead.
+    // Loads are issued unconditionally (a tile past the range re-reads the range's last
+    // tile) so that the compiler can count them: the wait before a tile's MFMAs then leaves
+    // the next tile's loads in flight.
+    const int last_tile = w.key_begin + ((w.key_end - 1 - w.key_begin) & ~31);
+    auto clamp_tile = [&](int x) { return x < w.key_end ? x : last_tile; };
+    // The block of the tile after next is read one iteration early, so the next tile's
+    // loads issue as soon as an iteration starts.
+    constexpr int stride = 4;
+    int t = w.key_begin + 32 * wave;
+    Tile cur, nxt;
+    fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
+    uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
+    for (; t < w.key_end; t += 32 * stride) {
+      const int tn = clamp_tile(t + 32 * stride);
+      fetch(tn, blk_next, nxt);
+      blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
+      // Issue the next tile's loads here, ahead of this tile's MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      consume(t, cur);
+      cur = nxt;
     }
-    float tmax = sc[0];
+  } else {
+    // Prefill blocks: every wave needs every tile, so the workgroup stages each 32-key
+    // tile once in LDS (double-buffered; the next tile's global loads are in flight while
+    // this one is used). Keys are rows of D + 8 halves (the pad spreads the permuted rows
+    // of a fragment over the LDS banks), values the tile's [D][32] sub-tile as stored.
+    constexpr int KROW = D + 8;
+    constexpr int STAGE = 32 * KROW + D * 32;  // halves per stage
+    constexpr int PIECES = D / 32;             // 16-byte pieces per thread per tile
+    _Float16* stage = reinterpret_cast<_Float16*>(smem);
+    half8 staged[PIECES];
+    auto load_tile = [&](int t) {
+      const uint64_t blk = block_of(t / bt);
+      const int off = t % bt;
+      const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
+      const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
 #pragma unroll
-    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sc[i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m, tmax);
-    const float base = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = rescale(m, base);
-    half8 pf;
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = sc[i] == -INFINITY ? 0.0f : expf(sc[i] - base);
-      psum += p;
-      pf[i] = to_half(p);
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-    m = m_new;
-    // A tile that runs past the key range reads cache slots no pass has written: zero
-    // them, since a zero probability does not cancel a non-finite value.
-    const bool tail = t + 32 > w.key_end;
-#pragma unroll
-    for (int df = 0; df < DF; ++df) {
-      o[df][0] *= alpha;
-      o[df][1] *= alpha;
-      o[df][2] *= alpha;
-      o[df][3] *= alpha;
-      half8 av = cur.v[df];
-      if (tail) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (t + 8 * quad + j >= w.key_end) av[j] = (_Float16)0.0f;
+      for (int q = 0; q < PIECES; ++q) {
+        const int e = threadIdx.x + q * kThreads;  // < 8 D: 4 D key pieces, then 4 D value pieces
+        staged[q] = e < 4 * D ? *reinterpret_cast<const half8*>(kb + (size_t)e * 8)
+                              : *reinterpret_cast<const half8*>(vb + (size_t)(e - 4 * D) * 8);
       }
-      o[df] = mfma(av, pf, o[df]);
+    };
+    auto store_tile = [&](int buffer) {
+      _Float16* dst = stage + buffer * STAGE;
+#pragma unroll
+      for (int q = 0; q < PIECES; ++q) {
+        const int e = threadIdx.x + q * kThreads;
+        if (e < 4 * D) {
+          const int row = e / (D / 8), c8 = e - row * (D / 8);
+          *reinterpret_cast<half8*>(dst + row * KROW + c8 * 8) = staged[q];
+        } else {
+          *reinterpret_cast<half8*>(dst + 32 * KROW + (e - 4 * D) * 8) = staged[q];
+        }
+      }
+    };
+    auto read_tile = [&](int buffer, Tile& f) {
+      const _Float16* ks = stage + buffer * STAGE;
+      const _Float16* vs = ks + 32 * KROW;
+      const int r0 = 8 * (col >> 2) + (col & 3);  // the permuted key rows of fetch()
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        f.k0[kk] = *reinterpret_cast<const half8*>(ks + r0 * KROW + 32 * kk + 8 * quad);
+        f.k1[kk] = *reinterpret_cast<const half8*>(ks + (r0 + 4) * KROW + 32 * kk + 8 * quad);
+      }
+#pragma unroll
+      for (int df = 0; df < DF; ++df) f.v[df] = *reinterpret_cast<const half8*>(vs + (16 * df + col) * 32 + 8 * quad);
+    };
+    const int tiles = (w.key_end - w.key_begin + 31) / 32;
+    load_tile(w.key_begin);
+    store_tile(0);
+    __syncthreads();
+    for (int i = 0; i < tiles; ++i) {
+      const int t = w.key_begin + 32 * i;
+      if (i + 1 < tiles) load_tile(t + 32);  // workgroup-uniform
+      Tile f;
+      read_tile(i & 1, f);
+      consume(t, f);
+      if (i + 1 < tiles) store_tile((i + 1) & 1);
+      __syncthreads();
     }
-    cur = nxt;
   }
 
   float m_fin = m, l_fin = l;
@@ -429,7 +501,9 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
 
 template <int D>
 void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
-  const size_t lds = (size_t)(128 + 4 * D * 16) * sizeof(float);
+  // The decode path's merge area and the prefill path's two K/V stages share the memory.
+  const size_t lds = std::max((size_t)(128 + 4 * D * 16) * sizeof(float),
+                              (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
   static const bool configured = [&] {
     HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
