@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
 // n_tile % 8, so all row tiles of one weight tile have the same id modulo 8 (one XCD, one
 // L2) and are dispatched together: the weight tile is read from HBM once.
 template <int MF, int NFW, int KC, int P, int PREC>
-__global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
+__global__ void __launch_bounds__(256, PREC == kF16 && MF <= 8 ? 2 : 1)
     gemm_xlds_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
   constexpr int BM = 16 * MF, BN = 64 * NFW, NT = 256;
   constexpr bool kLoA = PREC >= kSplitA, kLoB = PREC == kSplitAB;
@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(256, PREC == kF16 ? 2 : 1)
 
   // Staging of chunk c (k-steps kt0 + c*KC ...) into buffer c % 2: thread-strided pieces.
   // Activation rows past the operand's padding are not read: the operand is padded to the
-  // tile height by the caller (gemm_tile_rows).
+  // tile height by the caller (gemm_padded_rows).
   constexpr int PIECES = (CHUNK + NT - 1) / NT;
   half8 stage[PIECES];
   auto fetch_x = [&](int c) {
@@ -580,6 +580,7 @@ int launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int 
   const int m_tiles = (rows_bound + BM - 1) / BM;
   const int KT = (int)(a.Kp >> 5);
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
+  if ((uint64_t)m_tiles * BM > a.x_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the activation padding");
   const int tiles = n_tiles * m_tiles;
   int ksplit = 1;
   if (forced_ksplit > 0) {
@@ -615,6 +616,11 @@ int launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int 
 template <int MF, int NFW, int KC, int P>
 int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas,
                  int forced_ksplit) {
+  if constexpr (MF > 8) {
+    // Tiles above 128 rows hold their accumulators in AGPRs; the split-precision variants
+    // would need twice as many, so they run on 128-row tiles.
+    if (prec != kF16) return launch_xlds<8, NFW, KC, P>(stream, a, prec, rows_bound, target_ctas, forced_ksplit);
+  }
   constexpr int BM = 16 * MF, BN = 64 * NFW;
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
@@ -622,6 +628,7 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
   const int tiles = n_tiles * m_tiles;
   const int KT = (int)(a.Kp >> 5);
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
+  if ((uint64_t)m_tiles * BM > a.x_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the activation padding");
   int ksplit = forced_ksplit > 0 ? forced_ksplit : (tiles < target_ctas ? (target_ctas + tiles - 1) / tiles : 1);
   ksplit = std::min(ksplit, std::max(1, KT / (2 * KC)));
   ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
@@ -638,16 +645,20 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
     (void)configured;
     observed(name, [&] { kernel<<<grid, 256, lds, stream>>>(a, n_tiles, m_tiles, n_groups); });
   };
-  switch (prec) {
-    case kF16:
-      go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>, kernel_name<MF, NFW, KC, P, kF16>("gemm_xlds_kernel"));
-      break;
-    case kSplitA:
-      go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitA>, kernel_name<MF, NFW, KC, P, kSplitA>("gemm_xlds_kernel"));
-      break;
-    default:
-      go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>, kernel_name<MF, NFW, KC, P, kSplitAB>("gemm_xlds_kernel"));
-      break;
+  if constexpr (MF > 8) {
+    go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>, kernel_name<MF, NFW, KC, P, kF16>("gemm_xlds_kernel"));
+  } else {
+    switch (prec) {
+      case kF16:
+        go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>, kernel_name<MF, NFW, KC, P, kF16>("gemm_xlds_kernel"));
+        break;
+      case kSplitA:
+        go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitA>, kernel_name<MF, NFW, KC, P, kSplitA>("gemm_xlds_kernel"));
+        break;
+      default:
+        go(&gemm_xlds_kernel<MF, NFW, KC, P, kSplitAB>, kernel_name<MF, NFW, KC, P, kSplitAB>("gemm_xlds_kernel"));
+        break;
+    }
   }
   if (ksplit > 1 && a.defer_reduce) return ksplit;
   if (ksplit > 1) {
@@ -659,7 +670,6 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
 
 }  // namespace
 
-int gemm_tile_rows(int rows_bound) { return rows_bound <= 64 ? 64 : 128; }
 
 // Configuration table (ids are stable for the tuning harness):
 //   0..2: decode, BM = 16/32/64, BN = 64, four K-waves, ring of 4 k-steps
@@ -704,6 +714,8 @@ int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int r
     case 12:  // BM 64 x BN 256, chunks of 8, ring of 4
       return launch_xlds<4, 4, 8, 4>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
       break;
+    case 13:  // BM 192 x BN 256, chunks of 2, ring of 2 (accumulators in AGPRs, one wave per SIMD)
+      return launch_xlds<12, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
     default:
       return launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
       break;

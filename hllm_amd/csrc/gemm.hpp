@@ -20,6 +20,7 @@ struct GemmArgs {
   const int32_t* device_m;     // rows read on the device (sampled rows), <= the launch bound
   int N;                       // output features
   uint64_t w_rows_padded;      // weight rows allocated (tiles never read past them)
+  uint64_t x_rows_padded;      // activation rows allocated (row tiles never read past them)
   uint64_t Kp;                 // K padded to 32 (same for both operands)
   int ksplit;                  // set by the launcher
   float* workspace;            // split-K partial tiles
@@ -35,8 +36,9 @@ struct GemmArgs {
   uint64_t out_cols_padded;
 };
 
-// Rows of the tile a launch with `rows_bound` rows uses (activation buffers are padded to it).
-int gemm_tile_rows(int rows_bound);
+// Activation rows a buffer needs so that every row tile of a launch over up to `rows`
+// rows lies inside it (row tiles are at most 256 rows).
+inline uint64_t gemm_padded_rows(uint64_t rows) { return (rows + 256 + 127) / 128 * 128; }
 // Returns 0 when the epilogue has been applied, or (defer_reduce only) the number of K-split
 // partial output matrices left in the workspace for the consumer to sum in order.
 int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus);

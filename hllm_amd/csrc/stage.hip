@@ -236,7 +236,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   prec_ = !f32_exec ? kF16 : (w_f32_ ? kSplitAB : kSplitA);
   kv_f32_ = f32_exec;
   rows_max_ = c.max_pass_rows ? c.max_pass_rows : 2048;
-  rows_padded_ = pad_to(rows_max_, 128);
+  rows_padded_ = gemm_padded_rows(rows_max_);
   const uint64_t seq_max = c.max_sequences ? c.max_sequences : 512;
   items_max_ = std::min<uint64_t>(std::max<uint64_t>(seq_max, 1), 1024);
   const int bt = c.kv_block_tokens ? (int)c.kv_block_tokens : 64;
@@ -890,6 +890,7 @@ int Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const
   a.M = rows;
   a.N = n;
   a.w_rows_padded = w.rows_padded;
+  a.x_rows_padded = rows_padded_;
   a.Kp = w.cols_padded;
   a.workspace = gemm_ws_.as<float>();
   a.workspace_floats = gemm_ws_floats_;
