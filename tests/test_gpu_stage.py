@@ -4,7 +4,7 @@ through the C ABI.
 Tolerances: F32 execution 3e-5 and F16 execution 5e-3 on the tiny Transformers fixture
 (the reference's own CUDA-backend bars, hLLM tests/cpp/cuda_stage_test.cpp:102); synthetic
 Qwen3-shaped slices in F16 execution: max-abs <= 2e-2 and cosine >= 0.9999 against the F32
-CPU oracle; F32 execution (split-precision GEMMs, F32 KV): |d| <= 1e-4 + 1e-4 |expected|.
+CPU oracle; F32 execution (split-precision GEMMs, F32 KV): |d| <= 2e-4 + 1e-4 |expected|.
 """
 import numpy as np
 import pytest
