@@ -28,7 +28,7 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_length", "hllm_rocm_stage_execute", "hllm_rocm_stage_submit",
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
-           "hllm_rocm_stage_profile_records")
+           "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits")
 
 
 class StageError(RuntimeError):
@@ -117,6 +117,9 @@ def library() -> C.CDLL:
                                                C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                                C.POINTER(C.c_double)]
     L.hllm_rocm_stage_profile_records.argtypes = [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64)]
+    L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
+                                          C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
+                                          C.POINTER(C.c_double)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if fn.restype is C.c_int or (fn.restype is None and name != "hllm_rocm_stage_destroy"):
@@ -259,6 +262,13 @@ class Stage:
             p.cancelled = _ptr(cancelled, C.c_int32)
         out = {"tokens": np.zeros(n, np.uint64)}
         p.tokens = _ptr(out["tokens"], C.c_uint64)
+        if c.final_stage and any(it.flags & ITEM_LOGPROBS for it in items):
+            out["logprobs"] = np.full(n, np.nan)
+            out["top_ids"] = np.full((n, 5), np.iinfo(np.uint64).max, np.uint64)
+            out["top_logprobs"] = np.full((n, 5), np.nan)
+            p.logprobs = _ptr(out["logprobs"], C.c_double)
+            p.top_ids = _ptr(out["top_ids"], C.c_uint64)
+            p.top_logprobs = _ptr(out["top_logprobs"], C.c_double)
         if not c.final_stage:
             out["boundary"] = np.zeros((rows, c.hidden_size), np.uint16)
             p.boundary_out = _ptr(out["boundary"], C.c_uint16)
@@ -298,6 +308,25 @@ class Stage:
         buf = C.create_string_buffer(need.value)
         check(self.lib.hllm_rocm_stage_profile_records(self.handle, buf, need.value, C.byref(need)))
         return [r for r in buf.value.decode().split("\n") if r]
+
+
+def sample_logits(logits, options, device: int = 0):
+    """runtime::sample_token on the device for each row of `logits` ([rows, vocabulary]
+    F32) with the sampling fields of the matching Item of `options`: (tokens, logprobs,
+    top_ids [rows, 5], top_logprobs [rows, 5])."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    if lg.ndim != 2 or len(options) != lg.shape[0]:
+        raise ValueError("one option per row of [rows, vocabulary] logits")
+    rows, vocab = lg.shape
+    opts = (Item * rows)(*options)
+    tokens = np.zeros(rows, np.uint64)
+    logprobs = np.full(rows, np.nan)
+    top_ids = np.full((rows, 5), np.iinfo(np.uint64).max, np.uint64)
+    top_lp = np.full((rows, 5), np.nan)
+    check(library().hllm_rocm_sample_logits(device, _ptr(lg, C.c_float), rows, vocab, opts,
+                                             _ptr(tokens, C.c_uint64), _ptr(logprobs, C.c_double),
+                                             _ptr(top_ids, C.c_uint64), _ptr(top_lp, C.c_double)))
+    return tokens, logprobs, top_ids, top_lp
 
 
 def item(sequence: int, query_tokens: int, first_position: int, sample: bool = True,

@@ -167,6 +167,34 @@ void launch_argmax(hipStream_t stream, const float* logits, const int32_t* devic
                    int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
                    int32_t* flags);
 
+// Temperature / top-k / top-p sampling and log-probabilities of sampled rows whose item
+// asks for either (runtime::sample_token, cpp/src/sampling.cpp:19-89); greedy rows without
+// log-probabilities are left to the argmax. `tokens` holds each row's first maximum on
+// entry and the sampled token on exit.
+constexpr uint32_t kSampleLogprobs = 4;  // HLLM_ITEM_LOGPROBS
+struct SampleParams {
+  double temperature;
+  double top_p;
+  uint64_t top_k;
+  uint64_t seed;
+  uint64_t generated_index;
+  uint32_t top_logprobs;
+  uint32_t flags;
+};
+struct SampleArgs {
+  const float* logits;          // [rows][vocab]
+  int vocab;
+  int rows;
+  const SampleParams* params;   // [rows]
+  int32_t* tokens;              // [rows]
+  double* logprob;              // [rows]
+  int32_t* top_ids;             // [rows][5]
+  double* top_values;           // [rows][5]
+  double* weights;              // workspace [blocks][vocab]
+  uint32_t* lists;              // workspace [blocks][3][vocab]
+};
+void launch_sample(hipStream_t stream, const SampleArgs& a, int blocks);
+
 // Record sampled tokens as the sequences' last tokens (for HLLM_ITEM_TOKEN_FROM_DEVICE).
 void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,
                           const int32_t* sample_count, const ItemMeta* items, int32_t* last_token);

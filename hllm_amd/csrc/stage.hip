@@ -109,9 +109,12 @@ struct Profile {
 constexpr int kMaxSplits = 16;
 constexpr int kSplitUnit = 256;
 constexpr int kArgmaxParts = 64;
+constexpr int kSampleBlocks = 64;  // workgroups of the sampler (one row each at a time)
 constexpr uint64_t kStagingBytes = 64ull << 20;
 
 }  // namespace
+
+void check_sampling(const hllm_rocm_item& it);
 
 class Stage {
  public:
@@ -195,6 +198,10 @@ class Stage {
   int gemm_counter_count_ = 0;
   PackOut pack_{};
   PinnedMemory pin_items_, pin_tokens_, pin_out_tokens_, pin_flags_, pin_boundary_;
+  // sampler: per-row options, outputs [logprob: items][top values: items * 5][top IDs: items * 5]
+  DeviceMemory sample_params_, sample_out_, sample_weights_, sample_lists_;
+  PinnedMemory pin_sample_params_, pin_sample_out_;
+  int sample_blocks_ = 0;
 
   // in-flight pass
   bool in_flight_ = false;
@@ -202,6 +209,8 @@ class Stage {
   std::vector<uint32_t> pending_sequences_;
   std::vector<uint32_t> pending_lengths_;
   std::vector<int> pending_sample_items_;
+  std::vector<int> pending_top_counts_;  // per sampled row: -1 without log-probabilities
+  bool pending_sampler_ = false;
   uint64_t pending_rows_ = 0;
 
   bool profiling_ = false;
@@ -348,6 +357,11 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     logits_.allocate(items_max_ * V_ * sizeof(float), "logits");
     argmax_val_.allocate(items_max_ * kArgmaxParts * sizeof(float), "argmax");
     argmax_idx_.allocate(items_max_ * kArgmaxParts * sizeof(int32_t), "argmax");
+    sample_blocks_ = (int)std::min<uint64_t>(items_max_, kSampleBlocks);
+    sample_params_.allocate(items_max_ * sizeof(SampleParams), "sampling");
+    sample_out_.allocate(items_max_ * (6 * sizeof(double) + 5 * sizeof(int32_t)), "sampling");
+    sample_weights_.allocate((size_t)sample_blocks_ * V_ * sizeof(double), "sampling workspace");
+    sample_lists_.allocate((size_t)sample_blocks_ * 3 * V_ * sizeof(uint32_t), "sampling workspace");
   }
   tokens_.allocate(items_max_ * sizeof(int32_t), "tokens");
   flags_.allocate(sizeof(int32_t), "flags");
@@ -397,6 +411,8 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   pin_items_.allocate(items_max_ * sizeof(ItemMeta));
   pin_tokens_.allocate(R * sizeof(int32_t));
   pin_out_tokens_.allocate(items_max_ * sizeof(int32_t));
+  pin_sample_params_.allocate(items_max_ * sizeof(SampleParams));
+  pin_sample_out_.allocate(items_max_ * (6 * sizeof(double) + 5 * sizeof(int32_t)));
   pin_flags_.allocate(sizeof(int32_t));
   pin_boundary_.allocate(R * H_ * 2);
   staging_.allocate(kStagingBytes, "load staging");
@@ -929,6 +945,9 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   uint64_t rows = 0;
   std::vector<uint32_t> seqs(n);
   std::vector<int> sample_items;
+  std::vector<int> top_counts;
+  bool sampler = false;
+  SampleParams* params = pin_sample_params_.as<SampleParams>();
   {
     std::lock_guard<std::mutex> sl(seq_mutex_);
     std::set<uint32_t> unique;
@@ -944,12 +963,15 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       if ((it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) && (!c_.first_stage || it.query_tokens != 1 || s.length == 0))
         fail(HLLM_INVALID_REQUEST, "device-fed input needs one token of a started sequence");
       if (it.flags & HLLM_ITEM_SAMPLE) {
-        if (!(it.temperature >= 0.0 && it.temperature <= 100.0) || !(it.top_p > 0.0 && it.top_p <= 1.0) ||
-            it.top_logprobs > 5 || (!(it.flags & HLLM_ITEM_LOGPROBS) && it.top_logprobs != 0))
-          fail(HLLM_INVALID_REQUEST, "invalid sampling parameters");
-        if (it.temperature != 0.0 || (it.flags & HLLM_ITEM_LOGPROBS))
-          fail(HLLM_INCOMPATIBLE_WORKER, "device sampling supports greedy decoding only");
-        if (c_.final_stage) sample_items.push_back((int)i);
+        check_sampling(it);
+        if (c_.final_stage) {
+          const bool logprobs = (it.flags & HLLM_ITEM_LOGPROBS) != 0;
+          params[sample_items.size()] = {it.temperature, it.top_p, it.top_k, it.seed, it.generated_index,
+                                         logprobs ? it.top_logprobs : 0u, logprobs ? kSampleLogprobs : 0u};
+          sampler |= it.temperature != 0.0 || logprobs;
+          top_counts.push_back(logprobs ? (int)it.top_logprobs : -1);
+          sample_items.push_back((int)i);
+        }
       }
       seqs[i] = it.sequence;
       rows += it.query_tokens;
@@ -1116,6 +1138,24 @@ void Stage::submit(const hllm_rocm_pass& pass) {
           launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
                         argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_.as<int32_t>());
         });
+        if (sampler) {
+          HIP_CHECK(hipMemcpyAsync(sample_params_.ptr, pin_sample_params_.ptr, S * sizeof(SampleParams),
+                                   hipMemcpyHostToDevice, stream_));
+          SampleArgs sa{};
+          sa.logits = logits_.as<float>();
+          sa.vocab = (int)V_;
+          sa.rows = S;
+          sa.params = sample_params_.as<SampleParams>();
+          sa.tokens = tokens_.as<int32_t>();
+          sa.logprob = sample_out_.as<double>();
+          sa.top_values = sa.logprob + items_max_;
+          sa.top_ids = reinterpret_cast<int32_t*>(sa.top_values + 5 * items_max_);
+          sa.weights = sample_weights_.as<double>();
+          sa.lists = sample_lists_.as<uint32_t>();
+          timed("sample", (uint64_t)S * V_ * 4, 0.0, [&] { launch_sample(stream_, sa, sample_blocks_); });
+          HIP_CHECK(hipMemcpyAsync(pin_sample_out_.ptr, sample_out_.ptr, sample_out_.bytes, hipMemcpyDeviceToHost,
+                                   stream_));
+        }
         launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
                              items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
         HIP_CHECK(hipMemcpyAsync(pin_out_tokens_.ptr, tokens_.ptr, S * sizeof(int32_t), hipMemcpyDeviceToHost,
@@ -1143,6 +1183,8 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   pending_lengths_.assign(n, 0);
   for (uint32_t i = 0; i < n; ++i) pending_lengths_[i] = pass.item[i].query_tokens;
   pending_sample_items_ = sample_items;
+  pending_top_counts_ = top_counts;
+  pending_sampler_ = sampler;
   pending_rows_ = rows;
 }
 
@@ -1170,9 +1212,108 @@ void Stage::wait() {
     const int32_t* t = pin_out_tokens_.as<int32_t>();
     for (size_t j = 0; j < pending_sample_items_.size(); ++j) pass.tokens[pending_sample_items_[j]] = (uint64_t)t[j];
   }
+  if (c_.final_stage && pending_sampler_) {
+    const double* logprob = pin_sample_out_.as<double>();
+    const double* top_values = logprob + items_max_;
+    const int32_t* top_ids = reinterpret_cast<const int32_t*>(top_values + 5 * items_max_);
+    for (size_t j = 0; j < pending_sample_items_.size(); ++j) {
+      const int count = std::min(pending_top_counts_[j], (int)std::min<uint64_t>(V_, 5));
+      if (count < 0) continue;
+      const size_t item = (size_t)pending_sample_items_[j];
+      if (pass.logprobs) pass.logprobs[item] = logprob[j];
+      for (int r = 0; r < 5; ++r) {
+        if (pass.top_ids) pass.top_ids[item * 5 + r] = r < count ? (uint64_t)top_ids[j * 5 + r] : UINT64_MAX;
+        if (pass.top_logprobs)
+          pass.top_logprobs[item * 5 + r] = r < count ? top_values[j * 5 + r] : std::nan("");
+      }
+    }
+  }
   if (!c_.final_stage && pass.boundary_out) std::memcpy(pass.boundary_out, pin_boundary_.ptr, pending_rows_ * H_ * 2);
   std::lock_guard<std::mutex> sl(seq_mutex_);
   for (size_t i = 0; i < pending_sequences_.size(); ++i) sequences_[pending_sequences_[i]].length += pending_lengths_[i];
+}
+
+// The sampling options of one item, checked as runtime::validate_sampling
+// (cpp/src/sampling.cpp:10-17) does.
+void check_sampling(const hllm_rocm_item& it) {
+  if (!(it.temperature >= 0.0 && it.temperature <= 100.0) || !(it.top_p > 0.0 && it.top_p <= 1.0) ||
+      it.top_logprobs > 5 || (!(it.flags & HLLM_ITEM_LOGPROBS) && it.top_logprobs != 0))
+    fail(HLLM_INVALID_REQUEST, "invalid sampling parameters");
+}
+
+void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t V, const hllm_rocm_item* options,
+                   uint64_t* tokens, double* logprobs, uint64_t* top_ids, double* top_logprobs) {
+  if (!logits || !options || !tokens || rows == 0 || V == 0) fail(HLLM_INVALID_REQUEST, "invalid sampling request");
+  if (V > (1ull << 23) || rows > (1ull << 20)) fail(HLLM_RESOURCE_EXHAUSTED, "sampling request too large");
+  std::vector<SampleParams> params(rows);
+  for (uint64_t r = 0; r < rows; ++r) {
+    const hllm_rocm_item& it = options[r];
+    check_sampling(it);
+    const bool lp = (it.flags & HLLM_ITEM_LOGPROBS) != 0;
+    params[r] = {it.temperature, it.top_p, it.top_k, it.seed, it.generated_index, lp ? it.top_logprobs : 0u,
+                 lp ? kSampleLogprobs : 0u};
+  }
+  HIP_CHECK(hipSetDevice(device));
+  struct Stream {
+    hipStream_t s = nullptr;
+    ~Stream() {
+      if (s) (void)hipStreamDestroy(s);
+    }
+  } st;
+  HIP_CHECK(hipStreamCreate(&st.s));
+  const int blocks = (int)std::min<uint64_t>(rows, kSampleBlocks);
+  DeviceMemory d_logits, d_rows, d_tokens, d_flags, d_val, d_idx, d_params, d_out, d_w, d_lists;
+  d_logits.allocate(rows * V * sizeof(float), "logits");
+  d_rows.allocate(sizeof(int32_t), "sampling");
+  d_tokens.allocate(rows * sizeof(int32_t), "sampling");
+  d_flags.allocate(sizeof(int32_t), "sampling");
+  d_val.allocate(rows * kArgmaxParts * sizeof(float), "argmax");
+  d_idx.allocate(rows * kArgmaxParts * sizeof(int32_t), "argmax");
+  d_params.allocate(rows * sizeof(SampleParams), "sampling");
+  d_out.allocate(rows * (6 * sizeof(double) + 5 * sizeof(int32_t)), "sampling");
+  d_w.allocate((size_t)blocks * V * sizeof(double), "sampling workspace");
+  d_lists.allocate((size_t)blocks * 3 * V * sizeof(uint32_t), "sampling workspace");
+  const int32_t count = (int32_t)rows;
+  HIP_CHECK(hipMemcpyAsync(d_logits.ptr, logits, d_logits.bytes, hipMemcpyHostToDevice, st.s));
+  HIP_CHECK(hipMemcpyAsync(d_rows.ptr, &count, sizeof(count), hipMemcpyHostToDevice, st.s));
+  HIP_CHECK(hipMemcpyAsync(d_params.ptr, params.data(), d_params.bytes, hipMemcpyHostToDevice, st.s));
+  HIP_CHECK(hipMemsetAsync(d_flags.ptr, 0, sizeof(int32_t), st.s));
+  launch_argmax(st.s, d_logits.as<float>(), d_rows.as<int32_t>(), (int)rows, (int)V, d_val.as<float>(),
+                d_idx.as<int32_t>(), kArgmaxParts, d_tokens.as<int32_t>(), d_flags.as<int32_t>());
+  SampleArgs sa{};
+  sa.logits = d_logits.as<float>();
+  sa.vocab = (int)V;
+  sa.rows = (int)rows;
+  sa.params = d_params.as<SampleParams>();
+  sa.tokens = d_tokens.as<int32_t>();
+  sa.logprob = d_out.as<double>();
+  sa.top_values = sa.logprob + rows;
+  sa.top_ids = reinterpret_cast<int32_t*>(sa.top_values + 5 * rows);
+  sa.weights = d_w.as<double>();
+  sa.lists = d_lists.as<uint32_t>();
+  launch_sample(st.s, sa, blocks);
+  HIP_CHECK(hipGetLastError());
+  std::vector<int32_t> t(rows);
+  std::vector<unsigned char> out(d_out.bytes);
+  int32_t flags = 0;
+  HIP_CHECK(hipMemcpyAsync(t.data(), d_tokens.ptr, rows * sizeof(int32_t), hipMemcpyDeviceToHost, st.s));
+  HIP_CHECK(hipMemcpyAsync(out.data(), d_out.ptr, out.size(), hipMemcpyDeviceToHost, st.s));
+  HIP_CHECK(hipMemcpyAsync(&flags, d_flags.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, st.s));
+  HIP_CHECK(hipStreamSynchronize(st.s));
+  if (flags & 2) fail(HLLM_INTERNAL, "cannot sample nonfinite logits");
+  const double* lp = reinterpret_cast<const double*>(out.data());
+  const double* tv = lp + rows;
+  const int32_t* ti = reinterpret_cast<const int32_t*>(tv + 5 * rows);
+  for (uint64_t r = 0; r < rows; ++r) {
+    tokens[r] = (uint64_t)t[r];
+    if (!(params[r].flags & kSampleLogprobs)) continue;
+    const uint64_t n = std::min<uint64_t>(params[r].top_logprobs, V);
+    if (logprobs) logprobs[r] = lp[r];
+    for (uint64_t k = 0; k < 5; ++k) {
+      if (top_ids) top_ids[r * 5 + k] = k < n ? (uint64_t)ti[r * 5 + k] : UINT64_MAX;
+      if (top_logprobs) top_logprobs[r * 5 + k] = k < n ? tv[r * 5 + k] : std::nan("");
+    }
+  }
 }
 
 }  // namespace hllm_rocm
@@ -1299,6 +1440,14 @@ hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass
   const hllm_status s = hllm_rocm_stage_submit(stage, pass);
   if (s != HLLM_OK) return s;
   return hllm_rocm_stage_wait(stage);
+}
+
+hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t vocabulary,
+                                    const hllm_rocm_item* options, uint64_t* tokens, double* logprobs,
+                                    uint64_t* top_ids, double* top_logprobs) {
+  return guarded([&] {
+    hllm_rocm::sample_logits(device, logits, rows, vocabulary, options, tokens, logprobs, top_ids, top_logprobs);
+  });
 }
 
 hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, uint32_t rows,

@@ -34,8 +34,6 @@ struct RocmSequence final : runtime::SequenceState {
   }
 };
 
-bool greedy(const runtime::SamplingOptions& s) { return s.temperature == 0.0 && !s.return_logprobs; }
-
 std::uint32_t abi_dtype(runtime::DataType d) {
   switch (d) {
     case runtime::DataType::kF32: return HLLM_DTYPE_F32;
@@ -143,7 +141,8 @@ std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, b
   std::vector<RocmSequence*> states(n);
   std::vector<std::uint64_t> ids;
   std::vector<std::uint16_t> rows;
-  std::size_t total_rows = 0, host_sampled = 0;
+  std::size_t total_rows = 0;
+  bool logprobs = false;
   for (std::size_t i = 0; i < n; ++i) {
     auto* s = dynamic_cast<RocmSequence*>(members[i].state);
     if (!s || s->owner != this || s->failed || members[i].position != s->length)
@@ -172,9 +171,17 @@ std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, b
     it.first_position = members[i].position;
     it.top_p = 1.0;
     if (config_.final_stage && !s->prefill_only) {
-      runtime::validate_sampling(s->sampling);
-      it.flags = HLLM_ITEM_SAMPLE;
-      if (!greedy(s->sampling)) ++host_sampled;
+      // The device samples (cpp/src/cpu/stage.cpp:170-176 samples on the host).
+      const runtime::SamplingOptions& o = s->sampling;
+      runtime::validate_sampling(o);
+      it.flags = HLLM_ITEM_SAMPLE | (o.return_logprobs ? HLLM_ITEM_LOGPROBS : 0u);
+      it.top_logprobs = o.top_logprobs;
+      it.temperature = o.temperature;
+      it.top_p = o.top_p;
+      it.top_k = o.top_k;
+      it.seed = o.seed;
+      it.generated_index = s->generated_index;
+      logprobs |= o.return_logprobs;
     }
     total_rows += count;
   }
@@ -186,15 +193,18 @@ std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, b
   pass.token_ids = config_.first_stage ? ids.data() : nullptr;
   pass.boundary_in = config_.first_stage ? nullptr : rows.data();
   std::vector<std::uint64_t> tokens_out(n, 0);
-  std::vector<float> logits;
+  std::vector<double> logprob_out, top_out;
+  std::vector<std::uint64_t> top_ids_out;
   std::vector<std::uint16_t> boundary_out;
   if (config_.final_stage) {
     pass.tokens = tokens_out.data();
-    std::size_t sampled = 0;
-    for (const auto& it : items) sampled += (it.flags & HLLM_ITEM_SAMPLE) != 0;
-    if (host_sampled) {
-      logits.resize(sampled * config_.vocabulary_size);
-      pass.logits = logits.data();
+    if (logprobs) {
+      logprob_out.resize(n);
+      top_ids_out.resize(n * 5);
+      top_out.resize(n * 5);
+      pass.logprobs = logprob_out.data();
+      pass.top_ids = top_ids_out.data();
+      pass.top_logprobs = top_out.data();
     }
   } else {
     boundary_out.resize(total_rows * hidden);
@@ -208,20 +218,20 @@ std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, b
   std::vector<runtime::StageOutput> out;
   out.reserve(n);
   if (config_.final_stage) {
-    std::size_t sampled_row = 0;
     for (std::size_t i = 0; i < n; ++i) {
       RocmSequence* s = states[i];
       if (!(items[i].flags & HLLM_ITEM_SAMPLE)) {
         out.emplace_back(runtime::PrefillProgress{});
         continue;
       }
-      if (greedy(s->sampling)) {
-        out.emplace_back(runtime::SampledToken{tokens_out[i]});
-      } else {
-        const float* row = logits.data() + sampled_row * config_.vocabulary_size;
-        out.emplace_back(runtime::sample_token(row, config_.vocabulary_size, s->sampling, s->generated_index++));
+      runtime::SampledToken token{tokens_out[i]};
+      if (items[i].flags & HLLM_ITEM_LOGPROBS) {
+        token.logprob = logprob_out[i];
+        for (std::uint32_t r = 0; r < items[i].top_logprobs && top_ids_out[i * 5 + r] != UINT64_MAX; ++r)
+          token.top_logprobs.push_back({top_ids_out[i * 5 + r], top_out[i * 5 + r]});
       }
-      ++sampled_row;
+      ++s->generated_index;  // every sampled token advances the counter (cpp/src/cpu/stage.cpp:175)
+      out.emplace_back(std::move(token));
     }
   } else {
     std::size_t row = 0;

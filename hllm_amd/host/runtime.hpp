@@ -137,8 +137,9 @@ class StageBackend {
   }
 };
 
-// sampling.cpp:19-89 restated on the host (the device samples greedily; requests with a
-// temperature or log-probabilities are finished here from the stage's logits).
+// sampling.cpp:10-89 restated on the host, for callers that hold logits in host memory.
+// Stage passes sample on the device (hllm_rocm_stage_execute; hllm_rocm_sample_logits for
+// other logits), with the same options and counter.
 void validate_sampling(const SamplingOptions& options);
 std::uint64_t sample_logits(const float* logits, std::size_t count, const SamplingOptions& options,
                             std::uint64_t generated_index);

@@ -101,7 +101,10 @@ typedef struct {
   const volatile int32_t* cancelled; /* optional; polled between layers */
   /* outputs (host pointers; NULL = not wanted) */
   uint64_t* tokens;              /* final stage: [items]; items without SAMPLE get UINT64_MAX */
-  double* logprobs;              /* [items] with HLLM_ITEM_LOGPROBS */
+  /* For sampled items with HLLM_ITEM_LOGPROBS (runtime::SampledToken): the token's
+   * log-probability, and the top_logprobs best tokens and theirs in entries item * 5 + r,
+   * r < top_logprobs (later entries UINT64_MAX / NaN). Other items' entries are untouched. */
+  double* logprobs;              /* [items] */
   uint64_t* top_ids;             /* [items * 5] */
   double* top_logprobs;          /* [items * 5] */
   uint16_t* boundary_out;        /* non-final: [sum(query_tokens), hidden] F16 LE */
@@ -163,6 +166,17 @@ hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass
  * hllm_rocm_stage_wait. At most one pass is in flight per stage. */
 hllm_status hllm_rocm_stage_submit(hllm_rocm_stage* stage, const hllm_rocm_pass* pass);
 hllm_status hllm_rocm_stage_wait(hllm_rocm_stage* stage);
+
+/* runtime::sample_token (cpp/src/sampling.cpp:65-89) on the device for `rows` rows of
+ * `vocabulary` F32 logits (host memory), each with the sampling fields of options[r]
+ * (temperature, top_p, top_k, seed, generated_index; flags HLLM_ITEM_LOGPROBS and
+ * top_logprobs). The stage's sampler, for callers that hold logits of their own. Errors as
+ * the reference: invalid options are HLLM_INVALID_REQUEST, non-finite logits HLLM_INTERNAL.
+ * Outputs (host) as hllm_rocm_pass's; logprobs / top_ids / top_logprobs may be NULL. */
+hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_t rows,
+                                    uint64_t vocabulary, const hllm_rocm_item* options,
+                                    uint64_t* tokens, double* logprobs, uint64_t* top_ids,
+                                    double* top_logprobs);
 
 /* Diagnostics for parity tests, like the reference's traced execution
  * (cpp/include/hllm/cuda/stage.hpp:8-21): the last pass's device-built packing
