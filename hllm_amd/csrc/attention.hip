@@ -445,6 +445,9 @@ __global__ void __launch_bounds__(kThreads) attention_valu_kernel(AttentionArgs 
 // write the operand. Lane s < splits holds split s's statistics; lane L owns head
 // dimensions L*E .. L*E+E-1 (E = D / 64, at least 1). MFMA-path rows with a single split
 // were written by the attention kernel already.
+// The statistics and the first four splits' vectors are loaded together (unconditionally,
+// at clamped addresses): the kernel is a short latency-bound chain.
+template <int E>
 __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a, int mfma_path) {
   const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -462,8 +465,16 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
   }
   const int stride = D + 2;
   const float* part = partial_at(a, r, qh, 0);
-  const float ms = lane < splits ? part[lane * stride + D] : -INFINITY;
-  const float ls = lane < splits ? part[lane * stride + D + 1] : 0.0f;
+  const int dl = min(lane * E, D - E);  // lanes past D re-read the last elements
+  const float* stat = part + (size_t)min(lane, splits - 1) * stride + D;
+  const float ms_raw = stat[0], ls_raw = stat[1];
+  float pv[4][E];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int e = 0; e < E; ++e) pv[u][e] = part[(size_t)min(u, splits - 1) * stride + dl + e];
+  const float ms = lane < splits ? ms_raw : -INFINITY;
+  const float ls = lane < splits ? ls_raw : 0.0f;
   float m = ms;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -473,14 +484,25 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o, 64);
   const float inv = 1.0f / total;
-  const int E = D >= 64 ? D / 64 : 1;
-  if (lane * E < D) {
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) {
-      const float w = __shfl(ws, sp, 64);
-      const float* src = part + (size_t)sp * stride + lane * E;
-      for (int e = 0; e < E; ++e) v[e] += src[e] * w;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = 0.0f;
+  for (int sp0 = 0; sp0 < splits; sp0 += 4) {
+    if (sp0 > 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < E; ++e) pv[u][e] = part[(size_t)min(sp0 + u, splits - 1) * stride + dl + e];
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float w = __shfl(ws, min(sp0 + u, 63), 64);
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = sp0 + u < splits ? v[e] + pv[u][e] * w : v[e];
+    }
+  }
+  if (lane * E < D) {
+#pragma unroll
     for (int e = 0; e < E; ++e) {
       const float y = v[e] * inv;
       const uint64_t at = flayout_index(r, (uint64_t)qh * D + lane * E + e, a.out_cols_padded);
@@ -537,9 +559,16 @@ void launch_attention(hipStream_t stream, const AttentionArgs& a) {
     else
       observed("attention_valu_kernel<_Float16>", [&] { attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a); });
   }
-  const unsigned pairs = (unsigned)(a.rows * a.q_heads);
-  observed("attention_combine_kernel",
-           [&] { attention_combine_kernel<<<(pairs + 3) / 4, 256, 0, stream>>>(a, mfma_path ? 1 : 0); });
+  const unsigned blocks = (unsigned)(a.rows * a.q_heads + 3) / 4;
+  const int path = mfma_path ? 1 : 0;
+  observed("attention_combine_kernel", [&] {
+    if (a.head_dim <= 64)
+      attention_combine_kernel<1><<<blocks, 256, 0, stream>>>(a, path);
+    else if (a.head_dim <= 128)
+      attention_combine_kernel<2><<<blocks, 256, 0, stream>>>(a, path);
+    else
+      attention_combine_kernel<4><<<blocks, 256, 0, stream>>>(a, path);
+  });
 }
 
 }  // namespace hllm_rocm

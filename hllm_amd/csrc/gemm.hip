@@ -504,12 +504,28 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a, int n_tile
     float gate[8], up[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) gate[t] = up[t] = 0.0f;
-    for (int p = 0; p < a.ksplit; ++p) {
-      const float* src = ws + (size_t)p * BM * BN + m * BN + g * 64 + c8 * 8;
+    // Four splits' loads in flight at a time (clamped, unconditional), summed in split order.
+    const float* base = ws + m * BN + g * 64 + c8 * 8;
+    for (int p0 = 0; p0 < a.ksplit; p0 += 4) {
+      floatx4 q[4][4];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        gate[t] += src[t];
-        up[t] += src[32 + t];
+      for (int u = 0; u < 4; ++u) {
+        const float* src = base + (size_t)min(p0 + u, a.ksplit - 1) * BM * BN;
+        q[u][0] = *reinterpret_cast<const floatx4*>(src);
+        q[u][1] = *reinterpret_cast<const floatx4*>(src + 4);
+        q[u][2] = *reinterpret_cast<const floatx4*>(src + 32);
+        q[u][3] = *reinterpret_cast<const floatx4*>(src + 36);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool live = p0 + u < a.ksplit;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          gate[t] = live ? gate[t] + q[u][0][t] : gate[t];
+          gate[4 + t] = live ? gate[4 + t] + q[u][1][t] : gate[4 + t];
+          up[t] = live ? up[t] + q[u][2][t] : up[t];
+          up[4 + t] = live ? up[4 + t] + q[u][3][t] : up[4 + t];
+        }
       }
     }
     half8 vh, vl;
@@ -530,13 +546,23 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a, int n_tile
   float v[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) v[t] = 0.0f;
-#pragma unroll 4
-  for (int p = 0; p < a.ksplit; ++p) {
-    const float* src = ws + (size_t)p * BM * BN + m * BN + n;
-    const floatx4 x0 = *reinterpret_cast<const floatx4*>(src);
-    const floatx4 x1 = *reinterpret_cast<const floatx4*>(src + 4);
-    v[0] += x0[0]; v[1] += x0[1]; v[2] += x0[2]; v[3] += x0[3];
-    v[4] += x1[0]; v[5] += x1[1]; v[6] += x1[2]; v[7] += x1[3];
+  for (int p0 = 0; p0 < a.ksplit; p0 += 4) {
+    floatx4 q[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* src = ws + (size_t)min(p0 + u, a.ksplit - 1) * BM * BN + m * BN + n;
+      q[u][0] = *reinterpret_cast<const floatx4*>(src);
+      q[u][1] = *reinterpret_cast<const floatx4*>(src + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool live = p0 + u < a.ksplit;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[t] = live ? v[t] + q[u][0][t] : v[t];
+        v[4 + t] = live ? v[4 + t] + q[u][1][t] : v[4 + t];
+      }
+    }
   }
   float* out = a.out + (size_t)gm * a.ldo + gn;
 #pragma unroll

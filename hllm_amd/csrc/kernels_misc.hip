@@ -19,7 +19,7 @@ __device__ inline int wave_sum_int(int v) {
   return v;
 }
 
-// Sum over a 256-thread block in a fixed order (deterministic).
+// Sum over the block's waves in a fixed order (deterministic); scratch holds a float per wave.
 __device__ inline float block_sum(float v, float* scratch) {
   v = wave_sum(v);
   const int wave = threadIdx.x >> 6;
@@ -140,9 +140,6 @@ __global__ void boundary_encode_kernel(const float* h, uint64_t n, uint16_t* out
 
 // ------------------------------------------------------------------ RMSNorm -> operand
 
-// One block per row; each thread keeps its 8-column chunks in registers between the
-// square sum and the scaled store (hidden sizes up to 256 * 8 * kNormChunks).
-constexpr int kNormChunks = 4;
 __device__ inline void load8(const float* x, int c0, int hidden, bool vec, float* v) {
   if (vec && c0 < hidden) {
     const floatx4 a = *reinterpret_cast<const floatx4*>(x + c0);
@@ -154,63 +151,120 @@ __device__ inline void load8(const float* x, int c0, int hidden, bool vec, float
     for (int j = 0; j < 8; ++j) v[j] = c0 + j < hidden ? x[c0 + j] : 0.0f;
   }
 }
+__device__ inline void load8_at(const float* x, float* v) {
+  const floatx4 a = *reinterpret_cast<const floatx4*>(x);
+  const floatx4 b = *reinterpret_cast<const floatx4*>(x + 4);
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+}
 
-__global__ void __launch_bounds__(kBlock) rmsnorm_flayout_kernel(
+// One block per row; each thread owns Q chunks of 8 columns (blockDim = 64 * ceil(hidden /
+// 512) threads, at most 1024; Q = 2 above 8192 columns) and keeps them in registers
+// between the square sum and the scaled store. A row is a short chain of dependent steps,
+// so the kernel is latency-bound:
+// every load of a step (the chunks, or four K-split partials of every chunk) is issued
+// unconditionally, at clamped addresses, before any is used.
+template <int Q>
+__global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
     float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
     const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
     Partials residual) {
-  __shared__ float scratch[4];
+  __shared__ float scratch[16];
   const int r = blockIdx.x;
   const int count = device_rows ? *device_rows : rows;
   if (r >= count) return;
   const int src = row_index ? row_index[r] : r;
   float* x = h + (size_t)src * hidden;
-  float v[kNormChunks][8];
-  float squares = 0.0f;
-  const bool vec = (hidden & 7) == 0;
+  float v[Q][8];
+  int c0[Q];
 #pragma unroll
-  for (int q = 0; q < kNormChunks; ++q) {
-    const int c0 = (threadIdx.x + q * blockDim.x) * 8;
-    load8(x, c0, hidden, vec, v[q]);
-    if (residual.parts > 0 && c0 < hidden) {
-      // The projection's K-split partials summed in split order, then the residual add
-      // (the order of the reduce kernel's residual epilogue), written back in place.
-      float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < residual.parts; ++s) {
-        float p[8];
-        load8(residual.data + s * residual.stride + (size_t)src * hidden, c0, hidden, vec, p);
+  for (int q = 0; q < Q; ++q) c0[q] = (threadIdx.x + q * blockDim.x) * 8;
+  if ((hidden & 7) == 0) {
+    int c[Q];  // clamped chunk columns
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] += p[j];
+    for (int q = 0; q < Q; ++q) {
+      c[q] = min(c0[q], hidden - 8);
+      load8_at(x + c[q], v[q]);
+    }
+    if (residual.parts > 0) {
+      // The projection's K-split partials summed in split order from zero, then the
+      // residual add (the order of the reduce kernel's residual epilogue), written back.
+      float y[Q][8];
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[q][j] = 0.0f;
+      const float* base = residual.data + (size_t)src * hidden;
+      for (int s0 = 0; s0 < residual.parts; s0 += 4) {
+        float p[4][Q][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+            load8_at(base + (size_t)min(s0 + u, residual.parts - 1) * residual.stride + c[q], p[u][q]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[q][j] = s0 + u < residual.parts ? y[q][j] + p[u][q][j] : y[q][j];
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[q][j] += y[j];
-      if (vec) {
-        *reinterpret_cast<floatx4*>(x + c0) = floatx4{v[q][0], v[q][1], v[q][2], v[q][3]};
-        *reinterpret_cast<floatx4*>(x + c0 + 4) = floatx4{v[q][4], v[q][5], v[q][6], v[q][7]};
-      } else {
+      for (int q = 0; q < Q; ++q) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (c0 + j < hidden) x[c0 + j] = v[q][j];
+        for (int j = 0; j < 8; ++j) v[q][j] += y[q][j];
+        if (c0[q] < hidden) {
+          *reinterpret_cast<floatx4*>(x + c0[q]) = floatx4{v[q][0], v[q][1], v[q][2], v[q][3]};
+          *reinterpret_cast<floatx4*>(x + c0[q] + 4) = floatx4{v[q][4], v[q][5], v[q][6], v[q][7]};
+        }
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) squares += v[q][j] * v[q][j];
+    for (int q = 0; q < Q; ++q)
+      if (c0[q] >= hidden) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[q][j] = 0.0f;
+      }
+  } else {
+    // Hidden sizes that are not a multiple of 8 (test models): element-wise.
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      load8(x, c0[q], hidden, false, v[q]);
+      if (residual.parts > 0 && c0[q] < hidden) {
+        float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < residual.parts; ++s) {
+          float p[8];
+          load8(residual.data + s * residual.stride + (size_t)src * hidden, c0[q], hidden, false, p);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] += p[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          v[q][j] += y[j];
+          if (c0[q] + j < hidden) x[c0[q] + j] = v[q][j];
+        }
+      }
+    }
   }
+  float squares = 0.0f;
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) squares += v[q][j] * v[q][j];
   squares = block_sum(squares, scratch);
   const float inverse = 1.0f / sqrtf(squares / (float)hidden + eps);
 #pragma unroll
-  for (int q = 0; q < kNormChunks; ++q) {
-    const int c0 = (threadIdx.x + q * blockDim.x) * 8;
-    if (c0 >= (int)cols_padded) continue;
+  for (int q = 0; q < Q; ++q) {
+    if (c0[q] >= (int)cols_padded) continue;
     half8 vh, vl;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int c = c0 + j;
-      const float y = c < hidden ? (v[q][j] * inverse) * weight[c] : 0.0f;
+      const int cc = c0[q] + j;
+      const float y = cc < hidden ? (v[q][j] * inverse) * weight[cc] : 0.0f;
       vh[j] = to_half(y);
       vl[j] = to_half((y - (float)vh[j]) * kLoScale);
     }
-    const uint64_t at = flayout_index(r, c0, cols_padded);
+    const uint64_t at = flayout_index(r, c0[q], cols_padded);
     *reinterpret_cast<half8*>(out_hi + at) = vh;
     if (out_lo) *reinterpret_cast<half8*>(out_lo + at) = vl;
   }
@@ -229,6 +283,7 @@ __device__ inline uint64_t kv_index(const KvView& kv, int layer, int slot, int w
 // One wave per head. Lane l holds elements d = l + 64 j. Head dimensions are powers of two
 // in [4, 256]: for D >= 128 both members of a rotate-half pair (d, d + D/2) sit in the same
 // lane; for D <= 64 the partner is lane l ^ (D/2).
+template <int PER>  // elements per lane: ceil(D / 64)
 __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
     const float* qkv, int q_heads, int kv_heads, int head_dim, const float* q_norm,
     const float* k_norm, float eps, const float* rope_cos, const float* rope_sin,
@@ -239,7 +294,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   const int heads = q_heads + 2 * kv_heads;
   const int head_first = blockIdx.y * waves + wave;  // one head per wave
   const int D = head_dim, half = D / 2;
-  const int per_lane = D >= 64 ? D / 64 : 1;
+  constexpr int per_lane = PER;
   const int position = row_position[r];
   const int slot = row_slot[r];
   const float* row = qkv + (size_t)r * heads * D;
@@ -248,26 +303,37 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   for (int head = head_first; head < heads; head += waves * gridDim.y) {
     const bool is_q = head < q_heads;
     const bool is_v = head >= q_heads + kv_heads;
-    const float* src = row + head * D;
-    float v[4];
+    // Loads are unconditional (lanes past D re-read element D - 1) and every load of a step
+    // is in flight before any is used: the kernel is latency-bound.
+    int dd[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) dd[j] = min(lane + 64 * j, D - 1);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (parts.parts > 0) {
+      // K-split partials of the projection, summed in split order from zero (the reduce
+      // kernel's order for a plain store).
+      const size_t at = (size_t)r * heads * D + (size_t)head * D;
+      for (int s0 = 0; s0 < parts.parts; s0 += 4) {
+        float p[4][PER];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < PER; ++j)
+            p[u][j] = parts.data[(size_t)min(s0 + u, parts.parts - 1) * parts.stride + at + dd[j]];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < PER; ++j) v[j] = s0 + u < parts.parts ? v[j] + p[u][j] : v[j];
+      }
+    } else {
+      const float* src = row + head * D;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) v[j] = src[dd[j]];
+    }
     float squares = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = lane + 64 * j;
-      if (j < per_lane && d < D) {
-        if (parts.parts > 0) {
-          // K-split partials of the projection, summed in split order from zero (the
-          // reduce kernel's order for a plain store).
-          const size_t at = (size_t)r * heads * D + (size_t)head * D + d;
-          float y = 0.0f;
-          for (int s = 0; s < parts.parts; ++s) y += parts.data[s * parts.stride + at];
-          v[j] = y;
-        } else {
-          v[j] = src[d];
-        }
-      } else {
-        v[j] = 0.0f;
-      }
+    for (int j = 0; j < PER; ++j) {
+      if (lane + 64 * j >= D) v[j] = 0.0f;
       squares += v[j] * v[j];
     }
     if (!is_v) {
@@ -276,10 +342,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
         squares = wave_sum(squares);
         const float inverse = 1.0f / sqrtf(squares / (float)D + eps);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = lane + 64 * j;
-          if (j < per_lane && d < D) v[j] = v[j] * (inverse * w[d]);
-        }
+        for (int j = 0; j < PER; ++j) v[j] = v[j] * (inverse * w[dd[j]]);  // lanes past D hold 0
       }
       if (D >= 128) {
         const int pairs = per_lane / 2;  // elements [0, pairs) are first halves
@@ -522,8 +585,21 @@ void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int3
                             uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
                             Partials residual) {
   if (rows <= 0) return;
-  observed("rmsnorm_flayout_kernel", [&] { rmsnorm_flayout_kernel<<<rows, kBlock, 0, stream>>>(h, hidden, row_index, rows, device_rows,
-                                                      weight, eps, out_hi, out_lo, cols_padded, residual); });
+  // Chunks of 8 columns up to the padded width (the operand's zero padding is written too).
+  const int chunks = (int)((std::max<uint64_t>(hidden, cols_padded) + 7) / 8);
+  const int threads = std::min(1024, (chunks + 63) / 64 * 64);
+  if (chunks <= 1024) {
+    observed("rmsnorm_flayout_kernel<1>", [&] {
+      rmsnorm_flayout_kernel<1><<<rows, threads, 0, stream>>>(h, hidden, row_index, rows, device_rows, weight, eps,
+                                                             out_hi, out_lo, cols_padded, residual);
+    });
+  } else {
+    if (chunks > 2 * 1024) fail(HLLM_INTERNAL, "hidden size exceeds the RMSNorm kernel");
+    observed("rmsnorm_flayout_kernel<2>", [&] {
+      rmsnorm_flayout_kernel<2><<<rows, threads, 0, stream>>>(h, hidden, row_index, rows, device_rows, weight, eps,
+                                                             out_hi, out_lo, cols_padded, residual);
+    });
+  }
 }
 
 void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
@@ -532,9 +608,21 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
                             const int32_t* row_slot, KvView kv, int layer, float* q_out,
                             Partials qkv_parts) {
   const int heads = q_heads + 2 * kv_heads;
-  observed("qkv_rope_append_kernel", [&] { qkv_rope_append_kernel<<<dim3(rows, (heads + 3) / 4), kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm,
-                                                      k_norm, eps, rope_cos, rope_sin, row_position,
-                                                      row_slot, kv, layer, q_out, qkv_parts); });
+  const dim3 grid(rows, (heads + 3) / 4);
+  const auto go = [&](auto kernel) {
+    observed("qkv_rope_append_kernel", [&] {
+      kernel<<<grid, kBlock, 0, stream>>>(qkv, q_heads, kv_heads, head_dim, q_norm, k_norm, eps, rope_cos, rope_sin,
+                                          row_position, row_slot, kv, layer, q_out, qkv_parts);
+    });
+  };
+  if (head_dim <= 64)
+    go(&qkv_rope_append_kernel<1>);
+  else if (head_dim <= 128)
+    go(&qkv_rope_append_kernel<2>);
+  else if (head_dim <= 256)
+    go(&qkv_rope_append_kernel<4>);
+  else
+    fail(HLLM_INTERNAL, "head dimension exceeds the RoPE kernel");
 }
 
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
