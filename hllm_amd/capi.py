@@ -28,7 +28,8 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_length", "hllm_rocm_stage_execute", "hllm_rocm_stage_submit",
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
-           "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits")
+           "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
+           "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats")
 
 
 class StageError(RuntimeError):
@@ -117,6 +118,8 @@ def library() -> C.CDLL:
                                                C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                                C.POINTER(C.c_double)]
     L.hllm_rocm_stage_profile_records.argtypes = [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64)]
+    L.hllm_rocm_stage_set_graphs.argtypes = [vp, u32]
+    L.hllm_rocm_stage_graph_stats.argtypes = [vp, C.POINTER(u64), C.POINTER(u64)]
     L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
@@ -287,6 +290,17 @@ class Stage:
         check(self.lib.hllm_rocm_stage_execute(self.handle, C.byref(p)))
         del keep
         return out
+
+    # --------------------------------------------------------------- graphs
+    def set_graphs(self, enabled: bool) -> None:
+        """Replay repeated pass shapes from captured HIP graphs (default off)."""
+        check(self.lib.hllm_rocm_stage_set_graphs(self.handle, 1 if enabled else 0))
+
+    def graph_stats(self):
+        """(pass shapes captured, passes replayed from a graph)."""
+        cap, rep = C.c_uint64(), C.c_uint64()
+        check(self.lib.hllm_rocm_stage_graph_stats(self.handle, C.byref(cap), C.byref(rep)))
+        return cap.value, rep.value
 
     # --------------------------------------------------------------- profiling
     def profile(self, families: str | None) -> None:

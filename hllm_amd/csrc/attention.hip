@@ -53,11 +53,16 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 // ---------------------------------------------------------------- MFMA flash attention
 
 template <int D>
-__global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs a) {
+__global__ void __launch_bounds__(kThreads, D <= 128 ? 2 : 1) attention_mfma_kernel(AttentionArgs a) {
   constexpr int KK = D / 32;  // 32-wide chunks of the QK contraction
   constexpr int DF = D / 16;  // 16-row fragments of O^T
   extern __shared__ float smem[];
-  const AttnWork w = a.work[blockIdx.x];
+  // Workgroups loop over the work list (its size is written by the pack kernel); a launch
+  // may have fewer workgroups than items.
+  const int count = *a.work_count;
+  for (int wi = blockIdx.x; wi < count; wi += gridDim.x) {
+  [&] {
+  const AttnWork w = a.work[wi];
   const int kvh = blockIdx.y;
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
@@ -325,6 +330,9 @@ __global__ void __launch_bounds__(kThreads) attention_mfma_kernel(AttentionArgs 
       out[D + 1] = l_fin;
     }
   }
+  }();
+  __syncthreads();  // the next work item reuses the LDS
+  }
 }
 
 // ---------------------------------------------------------------- F32 VALU attention
@@ -532,7 +540,7 @@ void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
     return true;
   }();
   (void)configured;
-  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_count, a.kv_heads), kThreads, lds, stream>>>(a); });
+  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_grid, a.kv_heads), kThreads, lds, stream>>>(a); });
 }
 
 }  // namespace
@@ -545,7 +553,7 @@ void launch_attention(hipStream_t stream, const AttentionArgs& a) {
   if (a.rows <= 0) return;
   const bool mfma_path = attention_uses_mfma(a.head_dim, a.kv.f32 != 0);
   if (mfma_path) {
-    if (a.work_count > 0) {
+    if (a.work_grid > 0) {
       if (a.head_dim == 64) launch_mfma<64>(stream, a);
       if (a.head_dim == 128) launch_mfma<128>(stream, a);
       if (a.head_dim == 256) launch_mfma<256>(stream, a);

@@ -66,7 +66,9 @@ struct PackOut {
   int32_t* sample_item;    // [items]
   int32_t* sample_count;   // [1]
   AttnWork* attn_work;     // attention work items (MFMA path), in item order
+  int32_t* attn_count;     // [1] number of attention work items
   int32_t* row_splits;     // [rows] key splits of the row's attention block
+  int32_t* flags;          // [1] the pass's error flags, cleared by the pack kernel
   int attn_group;          // query heads per KV head
   int attn_max_splits;
   int attn_decode_unit;    // keys per split of decode-like blocks (attn_split_keys)
@@ -139,8 +141,9 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
 struct AttentionArgs {
   const float* q;              // [rows][Q][D]
   int rows, q_heads, kv_heads, head_dim;
-  const AttnWork* work;        // MFMA path work list and its host-computed size
-  int work_count;
+  const AttnWork* work;        // MFMA path work list, its size (device) and the launch's
+  const int32_t* work_count;   // workgroups along x, which loop over the list
+  int work_grid;
   const int32_t* row_splits;
   const int32_t* row_item;
   const int32_t* row_position;

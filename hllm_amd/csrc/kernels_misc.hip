@@ -66,6 +66,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
   const ItemMeta it = items[i];
   const bool sample = (it.flags & HLLM_ITEM_SAMPLE) != 0;
   if (threadIdx.x == 0) {
+    if (i == 0) *out.flags = 0;
     out.cu_seqlens[i] = offset;
     if (sample) {
       out.sample_row[samples] = offset + (int)it.query_tokens - 1;
@@ -101,6 +102,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
       }
       for (int r = 0; r < rows; ++r) out.row_splits[offset + r0 + r] = splits;
     }
+    if (i == n_items - 1) *out.attn_count = work;
   }
 }
 

@@ -11,6 +11,7 @@
 #include <mutex>
 #include <set>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "gemm.hpp"
@@ -110,6 +111,7 @@ constexpr int kMaxSplits = 16;
 constexpr int kSplitUnit = 256;
 constexpr int kArgmaxParts = 64;
 constexpr int kSampleBlocks = 64;  // workgroups of the sampler (one row each at a time)
+constexpr size_t kMaxGraphs = 16;  // captured pass shapes kept (least recently used dropped)
 constexpr uint64_t kStagingBytes = 64ull << 20;
 
 }  // namespace
@@ -139,6 +141,15 @@ class Stage {
   void read_kv(uint32_t handle, uint32_t layer, float* keys, float* values);
   void read_tensor(const std::string& name, float* out, uint64_t elements);
   void set_profiling(const std::string& families);
+  void set_graphs(bool enabled) {
+    std::lock_guard<std::mutex> lock(pass_mutex_);
+    graphs_enabled_ = enabled;
+  }
+  void graph_stats(uint64_t* captured, uint64_t* replayed) {
+    std::lock_guard<std::mutex> lock(pass_mutex_);
+    if (captured) *captured = graph_captures_;
+    if (replayed) *replayed = graph_replays_;
+  }
   void profile_read(const std::string& record, double* ms, uint64_t* launches, uint64_t* bytes, double* flops);
   std::string profile_records();
 
@@ -202,6 +213,30 @@ class Stage {
   DeviceMemory sample_params_, sample_out_, sample_weights_, sample_lists_;
   PinnedMemory pin_sample_params_, pin_sample_out_;
   int sample_blocks_ = 0;
+
+  // Passes whose shape (items, rows, sampled rows, sampler, attention work items) repeats
+  // can be replayed from a captured HIP graph (off by default: on MI355X the replay saves
+  // no measurable time on these passes, whose kernels, not their launches, set the pace).
+  // Every launch parameter of a pass is a function of its shape (all other per-pass values
+  // are read on the device); a shape is captured the second time it is seen (the first run
+  // sets the kernels' attributes eagerly).
+  struct PassShape {
+    uint32_t items, rows, samples, sampler, attention_items;
+    bool operator<(const PassShape& o) const {
+      return std::tie(items, rows, samples, sampler, attention_items) <
+             std::tie(o.items, o.rows, o.samples, o.sampler, o.attention_items);
+    }
+  };
+  struct CapturedPass {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  bool graphs_enabled_ = false;
+  std::map<PassShape, CapturedPass> graphs_;
+  std::set<PassShape> shapes_seen_;
+  uint64_t graph_clock_ = 0, graph_captures_ = 0, graph_replays_ = 0;
+  DeviceMemory attn_count_;
 
   // in-flight pass
   bool in_flight_ = false;
@@ -365,6 +400,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   }
   tokens_.allocate(items_max_ * sizeof(int32_t), "tokens");
   flags_.allocate(sizeof(int32_t), "flags");
+  pack_.flags = flags_.as<int32_t>();
   items_dev_.allocate(items_max_ * sizeof(ItemMeta), "items");
   host_tokens_dev_.allocate(R * sizeof(int32_t), "tokens");
   pack_buf_.allocate(((items_max_ + 1) + 5 * R + 2 * items_max_ + 1) * sizeof(int32_t), "pack");
@@ -396,11 +432,13 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     attn_work_max_ = (R / qb + items_max_) * kMaxSplits;
     attn_work_.allocate(attn_work_max_ * sizeof(AttnWork), "attention work");
     pack_.attn_work = attn_work_.as<AttnWork>();
+    attn_count_.allocate(sizeof(int32_t), "attention work");
+    pack_.attn_count = attn_count_.as<int32_t>();
     pack_.attn_group = (int)group;
     pack_.attn_max_splits = kMaxSplits;
     // Keys per split of decode-like attention blocks; HLLM_ROCM_ATTN_DECODE_SPLIT overrides
     // it for tuning (a multiple of 32).
-    pack_.attn_decode_unit = 256;
+    pack_.attn_decode_unit = 384;
     if (const char* v = std::getenv("HLLM_ROCM_ATTN_DECODE_SPLIT")) {
       const int unit = std::atoi(v);
       if (unit < 32 || unit % 32) fail(HLLM_INVALID_REQUEST, "HLLM_ROCM_ATTN_DECODE_SPLIT must be a multiple of 32");
@@ -453,6 +491,10 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
 Stage::~Stage() {
   if (stream_) {
     (void)hipStreamSynchronize(stream_);
+    for (auto& [shape, g] : graphs_) {
+      (void)hipGraphExecDestroy(g.exec);
+      (void)hipGraphDestroy(g.graph);
+    }
     for (auto& [name, p] : profiles_)
       for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
     for (auto e : event_pool_) (void)hipEventDestroy(e);
@@ -1027,12 +1069,15 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
 
-  // ---- device work
-  try {
-    const int R = (int)rows;
-    const int S = (int)sample_items.size();
+  // ---- device work. Every launch parameter below is a function of the pass shape (n, R,
+  // S, sampler): the rest is read on the device. `capturing`: recorded into a graph.
+  const int R = (int)rows;
+  const int S = (int)sample_items.size();
+  // One attention workgroup (per KV head) per work item: the hardware's dispatch balances
+  // items of different lengths.
+  const int attn_grid = attn_work_count;
+  auto enqueue = [&](bool capturing) {
     HIP_CHECK(hipMemcpyAsync(items_dev_.ptr, meta, n * sizeof(ItemMeta), hipMemcpyHostToDevice, stream_));
-    HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
     if (c_.first_stage)
       HIP_CHECK(hipMemcpyAsync(host_tokens_dev_.ptr, host_tokens, R * sizeof(int32_t), hipMemcpyHostToDevice,
                                stream_));
@@ -1065,7 +1110,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     float* ws = gemm_ws_.as<float>();
     Partials pending{};
     for (uint64_t l = 0; l < L_; ++l) {
-      if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+      if (!capturing && pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
       Layer& w = *layers_[l];
       timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.input_norm.as<float>(), eps, a0h, a0l,
@@ -1083,7 +1128,8 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       });
       AttentionArgs at{};
       at.work = attn_work_.as<AttnWork>();
-      at.work_count = attn_work_count;
+      at.work_count = attn_count_.as<int32_t>();
+      at.work_grid = attn_grid;
       at.row_splits = pack_.row_splits;
       at.q = q_.as<float>();
       at.rows = R;
@@ -1173,6 +1219,54 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     }
     HIP_CHECK(hipMemcpyAsync(pin_flags_.ptr, flags_.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
     HIP_CHECK(hipGetLastError());
+  };
+  try {
+    const PassShape shape{n, (uint32_t)R, (uint32_t)S, sampler ? 1u : 0u, (uint32_t)attn_grid};
+    const bool graphable = graphs_enabled_ && !profiling_ && !pass.logits && !pass.trace_hidden;
+    auto found = graphable ? graphs_.find(shape) : graphs_.end();
+    if (found != graphs_.end()) {
+      found->second.used = ++graph_clock_;
+      ++graph_replays_;
+      HIP_CHECK(hipGraphLaunch(found->second.exec, stream_));
+    } else if (graphable && shapes_seen_.count(shape)) {
+      CapturedPass cp;
+      HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+      try {
+        enqueue(true);
+      } catch (...) {
+        hipGraph_t dropped = nullptr;
+        (void)hipStreamEndCapture(stream_, &dropped);
+        if (dropped) (void)hipGraphDestroy(dropped);
+        throw;
+      }
+      HIP_CHECK(hipStreamEndCapture(stream_, &cp.graph));
+      const hipError_t e = hipGraphInstantiate(&cp.exec, cp.graph, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        (void)hipGraphDestroy(cp.graph);
+        graphs_enabled_ = false;  // this runtime cannot replay passes: run them eagerly
+        enqueue(false);
+      } else {
+        if (graphs_.size() >= kMaxGraphs) {
+          auto oldest = graphs_.begin();
+          for (auto g = graphs_.begin(); g != graphs_.end(); ++g)
+            if (g->second.used < oldest->second.used) oldest = g;
+          (void)hipGraphExecDestroy(oldest->second.exec);
+          (void)hipGraphDestroy(oldest->second.graph);
+          graphs_.erase(oldest);
+        }
+        cp.used = ++graph_clock_;
+        graphs_[shape] = cp;
+        ++graph_captures_;
+        ++graph_replays_;
+        HIP_CHECK(hipGraphLaunch(cp.exec, stream_));
+      }
+    } else {
+      if (graphable) {
+        if (shapes_seen_.size() >= 4096) shapes_seen_.clear();
+        shapes_seen_.insert(shape);
+      }
+      enqueue(false);
+    }
   } catch (...) {
     fail_pass(seqs);
     throw;
@@ -1448,6 +1542,14 @@ hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_
   return guarded([&] {
     hllm_rocm::sample_logits(device, logits, rows, vocabulary, options, tokens, logprobs, top_ids, top_logprobs);
   });
+}
+
+hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled) {
+  return guarded([&] { impl(stage).set_graphs(enabled != 0); });
+}
+
+hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured, uint64_t* replayed) {
+  return guarded([&] { impl(stage).graph_stats(captured, replayed); });
 }
 
 hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, uint32_t rows,

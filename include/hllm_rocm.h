@@ -178,6 +178,16 @@ hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_
                                     uint64_t* tokens, double* logprobs, uint64_t* top_ids,
                                     double* top_logprobs);
 
+/* Replay of repeated pass shapes (items, rows, sampled rows, sampler use, attention work
+ * items) from captured HIP graphs, off by default: a shape's second pass is captured and
+ * later ones replay it, with the same kernels and results as eager launches and less host
+ * launch work. Passes that request logits, traces or profiling run eagerly. No counterpart
+ * in the reference (its CUDA stage launches eagerly). Counters: shapes captured, passes
+ * replayed from a graph. */
+hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled);
+hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured,
+                                        uint64_t* replayed);
+
 /* Diagnostics for parity tests, like the reference's traced execution
  * (cpp/include/hllm/cuda/stage.hpp:8-21): the last pass's device-built packing
  * (cu_seqlens [items + 1], per-row positions and KV slots [rows]), a sequence's physical
