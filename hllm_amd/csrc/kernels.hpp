@@ -193,10 +193,22 @@ struct SampleArgs {
   double* logprob;              // [rows]
   int32_t* top_ids;             // [rows][5]
   double* top_values;           // [rows][5]
-  double* weights;              // workspace [blocks][vocab]
-  uint32_t* lists;              // workspace [blocks][3][vocab]
+  // Workspace for `group_rows` rows at a time (the rows are processed in groups):
+  double* weights;              // [group_rows][vocab] probabilities
+  uint8_t* buckets;             // [group_rows][bucket_stride] probability bucket per token
+  uint64_t bucket_stride;       // a multiple of 16, >= vocab
+  uint32_t* sorted;             // [group_rows][vocab] tokens grouped by bucket
+  uint32_t* lists;              // [group_rows][4][vocab] token lists
+  uint64_t* hist;               // [group_rows][256][3] zero between uses (the kernels clear it)
+  uint32_t* cursor;             // [group_rows][256] zero between uses (the kernels clear it)
+  double* lse_parts;            // [group_rows][chunks]
+  uint32_t* candidates;         // [group_rows][chunks][8] log-probability candidates
+  int group_rows;
+  int chunks;                   // first-pass workgroups per row (at most 64)
 };
-void launch_sample(hipStream_t stream, const SampleArgs& a, int blocks);
+// Workspace sizes for `group_rows` rows of `vocab` tokens.
+inline uint64_t sample_bucket_stride(uint64_t vocab) { return (vocab + 15) / 16 * 16; }
+void launch_sample(hipStream_t stream, const SampleArgs& a);
 
 // Record sampled tokens as the sequences' last tokens (for HLLM_ITEM_TOKEN_FROM_DEVICE).
 void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,

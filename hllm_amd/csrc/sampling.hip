@@ -1,17 +1,26 @@
-// Temperature / top-k / top-p sampling and log-probabilities on the device, one workgroup
-// per sampled row, following the reference sampler (cpp/src/sampling.cpp:19-89):
+// Temperature / top-k / top-p sampling and log-probabilities on the device, following the
+// reference sampler (cpp/src/sampling.cpp:19-89):
 //   p_i = exp((l_i - max) / T) in double; candidates in descending p, equal p by lower
 //   token ID; the first top_k of them; the shortest prefix whose mass reaches top_p of the
 //   candidates' total; a SplitMix64 counter draw u in [0, 1) times that prefix's mass picks
 //   the first candidate whose running mass exceeds it.
-// Nothing is sorted. Each cut is found by a radix descent over the candidates' rank
-// (~bits(p) << 32 | id, ascending = reference order): an 8-bit digit histogram of counts
-// and masses in LDS picks the digit bucket in which the running mass crosses the goal, that
-// bucket's members are compacted into a list, and the next digit below the list's highest
-// differing bit is examined, until one candidate remains.
+// Nothing is sorted by probability. A first kernel (many workgroups per row) computes
+// every p_i, its bucket (its binary exponent: buckets are ordered like the probabilities)
+// and each bucket's exact count and mass; a second one groups each row's tokens by bucket
+// (a counting sort). A third kernel (one workgroup per row) finds from the histogram the
+// bucket where each boundary (k-th candidate, top-p cut, draw) falls and the boundary
+// token inside that bucket's slice by a radix descent over their rank (~bits(p) << 32 |
+// id, ascending = reference order): an 8-bit digit histogram of counts and masses in LDS
+// picks the digit bucket in which the running mass crosses the goal, its members are
+// compacted, and the next digit below the list's highest differing bit is examined, until
+// one token remains.
+// Log-probabilities: the normaliser is summed per chunk and the chunks in order; the top
+// tokens are chosen from each chunk's eight best by logit, re-ranked by log-probability
+// (exact unless four tokens of one chunk with distinct logits round to the log-probability
+// of a chosen one).
 // Masses are sums of probabilities held as integers in units of 2^-80 (each probability is
 // in [0, 1]; a vocabulary of up to 2^23 sums without overflow), so every sum is exact and
-// independent of the order of the LDS atomics: results are deterministic. The reference
+// independent of the order of the atomics: results are deterministic. The reference
 // sums in sorted order in double; the two agree on the token except when the draw falls
 // within the reference's rounding error (about 1e-16 relative per term) of a boundary.
 #include "kernels.hpp"
@@ -34,6 +43,7 @@ struct Shared {
   int chosen;
   int never;
   u64 before_hi, before_lo;
+  u64 scan_count;
 };
 
 // ---------------------------------------------------------------- exact masses
@@ -123,18 +133,6 @@ __device__ inline void block_sum2(u64& x, u64& y, Shared& sh) {
   __syncthreads();
 }
 
-// A double sum in a fixed order: each wave's butterfly, then the waves in index order.
-__device__ inline double block_sum(double v, Shared& sh) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
-  if (lane_id() == 0) sh.dred[threadIdx.x >> 6] = v;
-  __syncthreads();
-  double total = 0.0;
-  for (int w = 0; w < kWaves; ++w) total += sh.dred[w];
-  __syncthreads();
-  return total;
-}
-
 // Append `e` to `out` when `keep` (one LDS atomic per wave; list order is arbitrary).
 __device__ inline void push(bool keep, uint32_t e, uint32_t* out, uint32_t* counter) {
   const u64 m = __ballot(keep);
@@ -144,6 +142,30 @@ __device__ inline void push(bool keep, uint32_t e, uint32_t* out, uint32_t* coun
   if (lane_id() == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
   base = __shfl(base, leader, 64);
   if (keep) out[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] = e;
+}
+
+// ---------------------------------------------------------------- list traversal
+
+// Visits the tokens of a list (nullptr: the identity list 0..n-1) kB per thread at a time,
+// with every load of a batch (list entries, then their probabilities) issued before any
+// is used: the traversals are latency-bound. f(token, probability) runs for each in order.
+constexpr int kB = 4;
+template <typename F>
+__device__ inline void for_each_token(const uint32_t* list, uint32_t n, const double* w, F&& f) {
+  for (uint32_t j0 = threadIdx.x; j0 < n; j0 += kThreads * kB) {
+    uint32_t e[kB];
+    double p[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const uint32_t j = min(j0 + (uint32_t)u * kThreads, n - 1);
+      e[u] = list ? list[j] : j;
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) p[u] = w[e[u]];
+#pragma unroll
+    for (int u = 0; u < kB; ++u)
+      if (j0 + (uint32_t)u * kThreads < n) f(e[u], p[u]);
+  }
 }
 
 // ---------------------------------------------------------------- radix descent
@@ -247,9 +269,7 @@ __device__ Found descend(const uint32_t* in, uint32_t n, u128 c_and, u128 c_or, 
       sh.lo[d] = 0;
     }
     __syncthreads();
-    for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-      const uint32_t e = cur ? cur[j] : j;
-      const double p = w[e];
+    for_each_token(cur, n, w, [&](uint32_t e, double p) {
       const int d = (int)((uint32_t)(rank_of(p, e) >> shift) & 255u);
       atomicAdd(&sh.count[d], 1u);
       if (kWeighted) {
@@ -257,7 +277,7 @@ __device__ Found descend(const uint32_t* in, uint32_t n, u128 c_and, u128 c_or, 
         atomicAdd(&sh.hi[d], f.hi);
         atomicAdd(&sh.lo[d], f.lo);
       }
-    }
+    });
     __syncthreads();
     if (threadIdx.x < 64) choose_bucket<kWeighted>(sh, before, goal, strict, never);
     __syncthreads();
@@ -265,14 +285,26 @@ __device__ Found descend(const uint32_t* in, uint32_t n, u128 c_and, u128 c_or, 
     before += fx_value(sh.before_hi, sh.before_lo);
     never = sh.never != 0;
     u128 a = ~(u128)0, o = 0;
-    for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-      const uint32_t e = cur ? cur[j] : j;
-      const u128 r = rank_of(w[e], e);
-      const bool keep = (int)((uint32_t)(r >> shift) & 255u) == chosen;
-      push(keep, e, out, &sh.list_n);
-      if (keep) {
-        a &= r;
-        o |= r;
+    // Wave-uniform trip counts keep every lane at the ballots of push().
+    for (uint32_t j0 = threadIdx.x & ~63u; j0 < n; j0 += kThreads * kB) {
+      uint32_t e[kB];
+      double p[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        const uint32_t j = min(j0 + lane_id() + (uint32_t)u * kThreads, n - 1);
+        e[u] = cur ? cur[j] : j;
+      }
+#pragma unroll
+      for (int u = 0; u < kB; ++u) p[u] = w[e[u]];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        const u128 r = rank_of(p[u], e[u]);
+        const bool keep = j0 + lane_id() + (uint32_t)u * kThreads < n && (int)((uint32_t)(r >> shift) & 255u) == chosen;
+        push(keep, e[u], out, &sh.list_n);
+        if (keep) {
+          a &= r;
+          o |= r;
+        }
       }
     }
     n = block_and_or(a, o, sh);  // its barriers also publish the list
@@ -299,18 +331,28 @@ __device__ uint32_t compact_upto(const uint32_t* in, uint32_t n, const double* w
   __syncthreads();
   u128 a = ~(u128)0, o = 0;
   u64 hi = 0, lo = 0;
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-    const uint32_t e = in ? in[j] : j;
-    const double p = w[e];
-    const u128 r = rank_of(p, e);
-    const bool keep = r <= limit;
-    push(keep, e, out, &sh.list_n);
-    if (keep) {
-      a &= r;
-      o |= r;
-      const Fx f = to_fx(p);
-      hi += f.hi;
-      lo += f.lo;
+  for (uint32_t j0 = threadIdx.x & ~63u; j0 < n; j0 += kThreads * kB) {
+    uint32_t e[kB];
+    double p[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const uint32_t j = min(j0 + lane_id() + (uint32_t)u * kThreads, n - 1);
+      e[u] = in ? in[j] : j;
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) p[u] = w[e[u]];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const u128 r = rank_of(p[u], e[u]);
+      const bool keep = j0 + lane_id() + (uint32_t)u * kThreads < n && r <= limit;
+      push(keep, e[u], out, &sh.list_n);
+      if (keep) {
+        a &= r;
+        o |= r;
+        const Fx f = to_fx(p[u]);
+        hi += f.hi;
+        lo += f.lo;
+      }
     }
   }
   const uint32_t listed = block_and_or(a, o, sh);
@@ -330,138 +372,478 @@ __device__ inline u64 counter_bits(u64 seed, u64 index) {
 
 __device__ inline bool rank_less(u64 ka, uint32_t ia, u64 kb, uint32_t ib) { return ka < kb || (ka == kb && ia < ib); }
 
-__global__ void __launch_bounds__(kThreads) sample_kernel(SampleArgs a) {
-  __shared__ Shared sh;
-  const uint32_t V = (uint32_t)a.vocab;
-  double* w = a.weights + (size_t)blockIdx.x * V;
-  uint32_t* b0 = a.lists + (size_t)blockIdx.x * 3 * V;
-  uint32_t* b1 = b0 + V;
-  uint32_t* b2 = b1 + V;
-  for (int s = blockIdx.x; s < a.rows; s += gridDim.x) {
-    const SampleParams p = a.params[s];
-    const bool want_logprobs = (p.flags & kSampleLogprobs) != 0;
-    if (!(p.temperature > 0.0) && !want_logprobs) continue;  // greedy: the first maximum stands
-    const float* lg = a.logits + (size_t)s * V;
-    int token = a.tokens[s];
-    const double best = (double)lg[token];
-    if (p.temperature > 0.0) {
-      u128 c_and = ~(u128)0, c_or = 0;
-      u64 hi = 0, lo = 0;
-      for (uint32_t i = threadIdx.x; i < V; i += kThreads) {
-        const double q = exp(((double)lg[i] - best) / p.temperature);
-        w[i] = q;
-        const u128 r = rank_of(q, i);
-        c_and &= r;
-        c_or |= r;
-        const Fx f = to_fx(q);
-        hi += f.hi;
-        lo += f.lo;
-      }
-      block_and_or(c_and, c_or, sh);  // barriers also publish w
-      block_sum2(hi, lo, sh);
-      u128 total = fx_value(hi, lo);
-      const uint32_t* cand = nullptr;
-      uint32_t cn = V;
-      if (p.top_k != 0 && p.top_k < (u64)V) {
-        const Found kth = descend<false>(nullptr, V, c_and, c_or, w, (u128)p.top_k, false, b0, b1, sh);
-        if (kth.id >= 0) {
-          cn = compact_upto(nullptr, V, w, rank_of(w[kth.id], (uint32_t)kth.id), b2, c_and, c_or, total, sh);
-          cand = b2;
-        }
-      }
-      const u128 threshold = fx_of(fx_double(total) * p.top_p);
-      const Found cut = descend<true>(cand, cn, c_and, c_or, w, threshold, false, b0, b1, sh);
-      if (cut.id >= 0) {
-        const double retained = fx_double(cut.running);
-        const double target = (double)(counter_bits(p.seed, p.generated_index) >> 11) * 0x1.0p-53 * retained;
-        u128 pa, po, pm;
-        const uint32_t pn = compact_upto(cand, cn, w, rank_of(w[cut.id], (uint32_t)cut.id), b0, pa, po, pm, sh);
-        const Found pick = descend<true>(b0, pn, pa, po, w, fx_of(target), true, b1, b2, sh);
-        if (pick.id >= 0) token = pick.id;
-      }
+// ---------------------------------------------------------------- probability buckets
+
+// Bucket of a probability: 1023 - its binary exponent, so ascending buckets hold
+// descending probabilities (every probability of bucket b exceeds every one of bucket
+// b + 1); probabilities below 2^-254, and zero, share the last bucket.
+constexpr int kBuckets = 256;
+constexpr int kCandidates = 8;  // log-probability candidates kept per chunk
+__device__ inline int bucket_of(double p) {
+  const int e = (int)(((u64)__double_as_longlong(p) >> 52) & 0x7ff);
+  const int b = 1023 - e;
+  return b < 0 ? 0 : (b > kBuckets - 1 ? kBuckets - 1 : b);
+}
+
+// Per-thread list of the kCandidates best (key, id) pairs seen, ascending.
+struct Best8 {
+  u64 k[kCandidates];
+  uint32_t i[kCandidates];
+  __device__ void clear() {
+#pragma unroll
+    for (int q = 0; q < kCandidates; ++q) {
+      k[q] = ~0ull;
+      i[q] = ~0u;
     }
-    if (threadIdx.x == 0) a.tokens[s] = token;
-    if (want_logprobs) {
-      // log-softmax of the raw logits (no temperature, no cuts)
-      double sum = 0.0;
-      for (uint32_t i = threadIdx.x; i < V; i += kThreads) sum += exp((double)lg[i] - best);
-      const double log_sum = log(block_sum(sum, sh));
-      if (threadIdx.x == 0) a.logprob[s] = ((double)lg[token] - best) - log_sum;
-      // the best top_logprobs tokens by (log-probability descending, ID ascending):
-      // per-thread sorted top 5, then one block-wide minimum per output
-      u64 tk[5];
-      uint32_t ti[5];
+  }
+  __device__ void offer(u64 key, uint32_t id) {
+    if (!rank_less(key, id, k[kCandidates - 1], i[kCandidates - 1])) return;
 #pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        tk[k] = ~0ull;
-        ti[k] = ~0u;
-      }
-      for (uint32_t i = threadIdx.x; i < V; i += kThreads) {
-        const u64 key = descending_key(((double)lg[i] - best) - log_sum);
-        if (!rank_less(key, i, tk[4], ti[4])) continue;
+    for (int q = kCandidates - 1; q > 0; --q) {
+      const bool below = rank_less(key, id, k[q - 1], i[q - 1]);
+      const bool here = !below && rank_less(key, id, k[q], i[q]);
+      k[q] = below ? k[q - 1] : here ? key : k[q];
+      i[q] = below ? i[q - 1] : here ? id : i[q];
+    }
+    if (rank_less(key, id, k[0], i[0])) {
+      k[0] = key;
+      i[0] = id;
+    }
+  }
+  __device__ void pop() {
 #pragma unroll
-        for (int k = 4; k > 0; --k) {
-          const bool below = rank_less(key, i, tk[k - 1], ti[k - 1]);
-          const bool here = !below && rank_less(key, i, tk[k], ti[k]);
-          tk[k] = below ? tk[k - 1] : here ? key : tk[k];
-          ti[k] = below ? ti[k - 1] : here ? i : ti[k];
-        }
-        if (rank_less(key, i, tk[0], ti[0])) {
-          tk[0] = key;
-          ti[0] = i;
-        }
-      }
-      const uint32_t rounds = min(p.top_logprobs, min(5u, V));
-      for (uint32_t r = 0; r < rounds; ++r) {
-        u64 k = tk[0];
-        uint32_t id = ti[0];
+    for (int q = 0; q < kCandidates - 1; ++q) {
+      k[q] = k[q + 1];
+      i[q] = i[q + 1];
+    }
+    k[kCandidates - 1] = ~0ull;
+    i[kCandidates - 1] = ~0u;
+  }
+};
+
+// The block-wide smallest (key, id) of the threads' offers (scratch: two u64 per wave).
+template <int kWavesInBlock>
+__device__ inline void block_min_pair(u64& key, uint32_t& id, u64 (*scratch)[4]) {
 #pragma unroll
-        for (int m = 32; m > 0; m >>= 1) {
-          const u64 ok = __shfl_xor(k, m, 64);
-          const uint32_t oi = __shfl_xor(id, m, 64);
-          if (rank_less(ok, oi, k, id)) {
-            k = ok;
-            id = oi;
-          }
-        }
-        if (lane_id() == 0) {
-          sh.red[threadIdx.x >> 6][0] = k;
-          sh.red[threadIdx.x >> 6][1] = id;
-        }
-        __syncthreads();
-        u64 bk = ~0ull;
-        uint32_t bi = ~0u;
-        for (int wv = 0; wv < kWaves; ++wv) {
-          if (rank_less(sh.red[wv][0], (uint32_t)sh.red[wv][1], bk, bi)) {
-            bk = sh.red[wv][0];
-            bi = (uint32_t)sh.red[wv][1];
-          }
-        }
-        __syncthreads();
-        if (tk[0] == bk && ti[0] == bi) {
+  for (int m = 32; m > 0; m >>= 1) {
+    const u64 ok = __shfl_xor(key, m, 64);
+    const uint32_t oi = __shfl_xor(id, m, 64);
+    if (rank_less(ok, oi, key, id)) {
+      key = ok;
+      id = oi;
+    }
+  }
+  if (lane_id() == 0) {
+    scratch[threadIdx.x >> 6][0] = key;
+    scratch[threadIdx.x >> 6][1] = id;
+  }
+  __syncthreads();
+  u64 bk = ~0ull;
+  uint32_t bi = ~0u;
+  for (int wv = 0; wv < kWavesInBlock; ++wv) {
+    if (rank_less(scratch[wv][0], (uint32_t)scratch[wv][1], bk, bi)) {
+      bk = scratch[wv][0];
+      bi = (uint32_t)scratch[wv][1];
+    }
+  }
+  __syncthreads();
+  key = bk;
+  id = bi;
+}
+
+// First pass, one chunk of one row's vocabulary per workgroup (grid: chunks x rows): the
+// probabilities (kept for the later passes), each token's bucket, and the exact count and
+// mass of every bucket, added to the row's histogram with integer atomics (so the sums do
+// not depend on their order); for log-probabilities, the chunk's share of the normaliser
+// and its kCandidates best tokens by (logit - max) descending, ID ascending.
+constexpr int kPassThreads = 256;
+constexpr int kPassWaves = kPassThreads / 64;
+__global__ void __launch_bounds__(kPassThreads) sample_histogram_kernel(SampleArgs a, int row0) {
+  __shared__ uint32_t cnt[kBuckets];
+  __shared__ u64 hi[kBuckets], lo[kBuckets];
+  __shared__ double dred[kPassWaves];
+  __shared__ u64 pred[kPassWaves][4];
+  const int r = blockIdx.y, s = row0 + r;
+  if (s >= a.rows) return;
+  const SampleParams p = a.params[s];
+  const bool sampled = p.temperature > 0.0, logprobs = (p.flags & kSampleLogprobs) != 0;
+  if (!sampled && !logprobs) return;
+  const uint32_t V = (uint32_t)a.vocab;
+  const float* lg = a.logits + (size_t)s * V;
+  const double best = (double)lg[a.tokens[s]];
+  const uint32_t per = (V + gridDim.x - 1) / gridDim.x;
+  const uint32_t i0 = blockIdx.x * per, i1 = min(V, i0 + per);
+  double* w = a.weights + (size_t)r * V;
+  uint8_t* bk = a.buckets + (size_t)r * a.bucket_stride;
+  for (int b = threadIdx.x; b < kBuckets; b += kPassThreads) {
+    cnt[b] = 0;
+    hi[b] = 0;
+    lo[b] = 0;
+  }
+  __syncthreads();
+  double lse = 0.0;
+  Best8 top;
+  top.clear();
+  for (uint32_t i = i0 + threadIdx.x; i < i1; i += kPassThreads) {
+    const double l = (double)lg[i] - best;
+    if (sampled) {
+      const double q = exp(l / p.temperature);
+      w[i] = q;
+      const int b = bucket_of(q);
+      bk[i] = (uint8_t)b;
+      const Fx f = to_fx(q);
+      atomicAdd(&cnt[b], 1u);
+      if (f.hi) atomicAdd(&hi[b], f.hi);
+      if (f.lo) atomicAdd(&lo[b], f.lo);
+    }
+    if (logprobs) {
+      lse += exp(l);
+      top.offer(descending_key(l), i);
+    }
+  }
+  __syncthreads();
+  if (sampled) {
+    u64* h = reinterpret_cast<u64*>(a.hist) + (size_t)r * kBuckets * 3;
+    for (int b = threadIdx.x; b < kBuckets; b += kPassThreads) {
+      if (cnt[b] == 0) continue;
+      atomicAdd(&h[b * 3 + 0], (u64)cnt[b]);
+      atomicAdd(&h[b * 3 + 1], hi[b]);
+      atomicAdd(&h[b * 3 + 2], lo[b]);
+    }
+  }
+  if (logprobs) {
+    // fixed order: each wave's butterfly, then the waves in index order
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            tk[q] = tk[q + 1];
-            ti[q] = ti[q + 1];
-          }
-          tk[4] = ~0ull;
-          ti[4] = ~0u;
-        }
-        if (threadIdx.x == 0 && bi < V) {
-          a.top_ids[(size_t)s * 5 + r] = (int32_t)bi;
-          a.top_values[(size_t)s * 5 + r] = ((double)lg[bi] - best) - log_sum;
-        }
-      }
+    for (int m = 32; m > 0; m >>= 1) lse += __shfl_xor(lse, m, 64);
+    if ((threadIdx.x & 63) == 0) dred[threadIdx.x >> 6] = lse;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double t = 0.0;
+      for (int q = 0; q < kPassWaves; ++q) t += dred[q];
+      a.lse_parts[(size_t)r * gridDim.x + blockIdx.x] = t;
+    }
+    uint32_t* out = a.candidates + ((size_t)r * gridDim.x + blockIdx.x) * kCandidates;
+    for (int q = 0; q < kCandidates; ++q) {
+      u64 key = top.k[0];
+      uint32_t id = top.i[0];
+      block_min_pair<kPassWaves>(key, id, pred);
+      if (top.k[0] == key && top.i[0] == id) top.pop();
+      if (threadIdx.x == 0) out[q] = id;  // ~0u past the chunk's end
+    }
+  }
+}
+
+// Wave 0: exclusive prefix of the 256 bucket counts into `off`.
+__device__ inline void bucket_offsets(const uint32_t* cnt, uint32_t* off) {
+  const int lane = threadIdx.x;
+  uint32_t c[4], t = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    c[k] = cnt[lane * 4 + k];
+    t += c[k];
+  }
+  uint32_t e = t;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(e, o, 64);
+    if (lane >= o) e += v;
+  }
+  e -= t;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    off[lane * 4 + k] = e;
+    e += c[k];
+  }
+}
+
+// Second pass (grid: chunks x rows): a counting sort of each row's tokens by bucket into
+// `sorted` (bucket b's tokens at [offset(b), offset(b) + count(b)), in no particular
+// order; every use of a bucket is order-independent).
+__global__ void __launch_bounds__(kPassThreads) sample_scatter_kernel(SampleArgs a, int row0) {
+  __shared__ uint32_t off[kBuckets], local[kBuckets], base[kBuckets];
+  const int r = blockIdx.y, s = row0 + r;
+  if (s >= a.rows) return;
+  if (!(a.params[s].temperature > 0.0)) return;
+  const uint32_t V = (uint32_t)a.vocab;
+  const uint32_t per = (V + gridDim.x - 1) / gridDim.x;
+  const uint32_t i0 = blockIdx.x * per, i1 = min(V, i0 + per);
+  const uint8_t* bk = a.buckets + (size_t)r * a.bucket_stride;
+  const u64* h = reinterpret_cast<const u64*>(a.hist) + (size_t)r * kBuckets * 3;
+  uint32_t* cursor = a.cursor + (size_t)r * kBuckets;
+  uint32_t* sorted = a.sorted + (size_t)r * V;
+  for (int b = threadIdx.x; b < kBuckets; b += kPassThreads) {
+    local[b] = (uint32_t)h[b * 3];  // the row's counts, for the offsets
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) bucket_offsets(local, off);
+  __syncthreads();
+  for (int b = threadIdx.x; b < kBuckets; b += kPassThreads) local[b] = 0;
+  __syncthreads();
+  for (uint32_t i = i0 + threadIdx.x; i < i1; i += kPassThreads) atomicAdd(&local[bk[i]], 1u);
+  __syncthreads();
+  for (int b = threadIdx.x; b < kBuckets; b += kPassThreads) {
+    base[b] = local[b] ? off[b] + atomicAdd(&cursor[b], local[b]) : 0;
+    local[b] = 0;
+  }
+  __syncthreads();
+  for (uint32_t i = i0 + threadIdx.x; i < i1; i += kPassThreads) {
+    const int b = bk[i];
+    sorted[base[b] + atomicAdd(&local[b], 1u)] = i;
+  }
+}
+
+struct BucketPick {
+  int bucket;    // the first bucket reaching the goal; `limit` when none below it does
+  u64 count;     // tokens in the buckets before it
+  u128 mass;     // their mass
+};
+
+// Wave 0: the first bucket b < limit at which the running count (or mass) of buckets
+// 0..b reaches `goal` (>= goal, or > goal when `strict`). Result in LDS.
+__device__ void scan_buckets(const uint32_t* cnt, const u64* hi, const u64* lo, int limit, u128 goal, bool counts,
+                             bool strict, Shared& sh) {
+  const int lane = threadIdx.x;
+  u64 c[4], h[4], l[4];
+  u64 lc = 0, lh = 0, ll = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int d = lane * 4 + k;
+    const bool in = d < limit;
+    c[k] = in ? cnt[d] : 0;
+    h[k] = in ? hi[d] : 0;
+    l[k] = in ? lo[d] : 0;
+    lc += c[k];
+    lh += h[k];
+    ll += l[k];
+  }
+  u64 ec = lc, eh = lh, el = ll;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const u64 tc = __shfl_up(ec, off, 64), th = __shfl_up(eh, off, 64), tl = __shfl_up(el, off, 64);
+    if (lane >= off) {
+      ec += tc;
+      eh += th;
+      el += tl;
+    }
+  }
+  ec -= lc;
+  eh -= lh;
+  el -= ll;
+  int hit = -1;
+  u64 hc = 0, hh = 0, hl = 0;
+  u64 rc = ec, rh = eh, rl = el;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u128 incl = counts ? (u128)(rc + c[k]) : fx_value(rh + h[k], rl + l[k]);
+    if (hit < 0 && c[k] > 0 && (strict ? incl > goal : incl >= goal)) {
+      hit = k;
+      hc = rc;
+      hh = rh;
+      hl = rl;
+    }
+    rc += c[k];
+    rh += h[k];
+    rl += l[k];
+  }
+  const u64 hits = __ballot(hit >= 0);
+  if (hits) {
+    if (lane == __builtin_ctzll(hits)) {
+      sh.chosen = lane * 4 + hit;
+      sh.before_hi = hh;
+      sh.before_lo = hl;
+      sh.scan_count = hc;
+    }
+  } else if (lane == 63) {
+    sh.chosen = limit;
+    sh.before_hi = rh;
+    sh.before_lo = rl;
+    sh.scan_count = rc;
+  }
+}
+
+__device__ BucketPick pick_bucket(const uint32_t* cnt, const u64* hi, const u64* lo, int limit, u128 goal, bool counts,
+                                  bool strict, Shared& sh) {
+  if (threadIdx.x < 64) scan_buckets(cnt, hi, lo, limit, goal, counts, strict, sh);
+  __syncthreads();
+  const BucketPick b{sh.chosen, sh.scan_count, fx_value(sh.before_hi, sh.before_lo)};
+  __syncthreads();
+  return b;
+}
+
+// AND / OR of the ranks of a list's tokens.
+__device__ void list_ranks(const uint32_t* list, uint32_t n, const double* w, u128& c_and, u128& c_or, Shared& sh) {
+  u128 an = ~(u128)0, o = 0;
+  for_each_token(list, n, w, [&](uint32_t e, double p) {
+    const u128 r = rank_of(p, e);
+    an &= r;
+    o |= r;
+  });
+  block_and_or(an, o, sh);
+  c_and = an;
+  c_or = o;
+}
+
+// Third pass, one row per workgroup: the token, by exact descents over the bucket slices
+// where the top-k, top-p and draw boundaries fall; then log-probabilities.
+__global__ void __launch_bounds__(kThreads) sample_select_kernel(SampleArgs a, int row0) {
+  __shared__ Shared sh;
+  __shared__ uint32_t bcnt[kBuckets], boff[kBuckets];
+  __shared__ u64 bhi[kBuckets], blo[kBuckets];
+  const int r = blockIdx.x, s = row0 + r;
+  if (s >= a.rows) return;
+  const SampleParams p = a.params[s];
+  const bool sampled = p.temperature > 0.0, logprobs = (p.flags & kSampleLogprobs) != 0;
+  if (!sampled && !logprobs) return;  // greedy: the first maximum stands
+  const uint32_t V = (uint32_t)a.vocab;
+  const float* lg = a.logits + (size_t)s * V;
+  int token = a.tokens[s];
+  const double best = (double)lg[token];
+  if (sampled) {
+    const double* w = a.weights + (size_t)r * V;
+    const uint32_t* sorted = a.sorted + (size_t)r * V;
+    uint32_t* L[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L[q] = a.lists + ((size_t)r * 4 + q) * V;
+    // The row's histogram and sort cursors, cleared for their next use.
+    u64* h = reinterpret_cast<u64*>(a.hist) + (size_t)r * kBuckets * 3;
+    uint32_t* cursor = a.cursor + (size_t)r * kBuckets;
+    for (int b = threadIdx.x; b < kBuckets; b += kThreads) {
+      bcnt[b] = (uint32_t)h[b * 3 + 0];
+      bhi[b] = h[b * 3 + 1];
+      blo[b] = h[b * 3 + 2];
+      h[b * 3 + 0] = 0;
+      h[b * 3 + 1] = 0;
+      h[b * 3 + 2] = 0;
+      cursor[b] = 0;
     }
     __syncthreads();
+    if (threadIdx.x < 64) bucket_offsets(bcnt, boff);
+    __syncthreads();
+    auto slice = [&](int b) { return sorted + boff[b]; };
+    // 1. Candidates: the first top_k in rank order (all tokens when top_k is 0 or >= V).
+    //    Buckets below kb are whole; bucket kb contributes the list `kl` (nk tokens).
+    int kb = kBuckets;
+    u128 kb_mass = 0;  // mass of the buckets before kb
+    uint32_t* kl = nullptr;
+    uint32_t nk = 0;
+    u128 k_and = 0, k_or = 0, total;
+    if (p.top_k != 0 && p.top_k < (u64)V) {
+      const BucketPick kp = pick_bucket(bcnt, bhi, blo, kBuckets, (u128)p.top_k, true, false, sh);
+      kb = kp.bucket;
+      kb_mass = kp.mass;
+      u128 an, o;
+      const uint32_t n = bcnt[kb];
+      list_ranks(slice(kb), n, w, an, o, sh);
+      const Found kth = descend<false>(slice(kb), n, an, o, w, (u128)(p.top_k - kp.count), false, L[2], L[3], sh);
+      u128 km = 0;
+      if (kth.id >= 0) nk = compact_upto(slice(kb), n, w, rank_of(w[kth.id], (uint32_t)kth.id), L[0], k_and, k_or, km, sh);
+      kl = L[0];
+      total = kb_mass + km;
+    } else {
+      total = pick_bucket(bcnt, bhi, blo, kBuckets, ~(u128)0, false, false, sh).mass;
+    }
+    // 2. The top-p cut: the first candidate whose running mass reaches total * top_p.
+    const u128 threshold = fx_of(fx_double(total) * p.top_p);
+    const BucketPick cp = pick_bucket(bcnt, bhi, blo, kb, threshold, false, false, sh);
+    const uint32_t* cl;  // the cut's bucket slice (or its candidates in bucket kb)
+    uint32_t nc;
+    int cut_bucket;
+    u128 c_and, c_or, c_before, goal = threshold;
+    if (cp.bucket < kb) {
+      cut_bucket = cp.bucket;
+      cl = slice(cut_bucket);
+      nc = bcnt[cut_bucket];
+      list_ranks(cl, nc, w, c_and, c_or, sh);
+      c_before = cp.mass;
+    } else if (kb < kBuckets) {
+      cut_bucket = kb;
+      cl = kl;
+      nc = nk;
+      c_and = k_and;
+      c_or = k_or;
+      c_before = kb_mass;
+    } else {
+      // Rounding put the threshold above the whole mass: every candidate is retained,
+      // and the cut is the last one (the reference's loop runs to the end).
+      cut_bucket = kBuckets - 1;
+      while (cut_bucket > 0 && bcnt[cut_bucket] == 0) --cut_bucket;
+      cl = slice(cut_bucket);
+      nc = bcnt[cut_bucket];
+      list_ranks(cl, nc, w, c_and, c_or, sh);
+      c_before = total - fx_value(bhi[cut_bucket], blo[cut_bucket]);
+      goal = ~(u128)0;
+    }
+    const Found cut =
+        descend<true>(cl, nc, c_and, c_or, w, goal == ~(u128)0 ? goal : goal - c_before, false, L[2], L[3], sh);
+    if (cut.id >= 0) {
+      const u128 retained = c_before + cut.running;
+      // 3. The draw: the first retained candidate whose running mass exceeds u * retained.
+      const double target = (double)(counter_bits(p.seed, p.generated_index) >> 11) * 0x1.0p-53 * fx_double(retained);
+      const u128 x = fx_of(target);
+      const BucketPick pp = pick_bucket(bcnt, bhi, blo, cut_bucket, x, false, true, sh);
+      Found pick{-1, 0};
+      if (pp.bucket < cut_bucket) {
+        u128 an, o;
+        const uint32_t n = bcnt[pp.bucket];
+        list_ranks(slice(pp.bucket), n, w, an, o, sh);
+        pick = descend<true>(slice(pp.bucket), n, an, o, w, x - pp.mass, true, L[2], L[3], sh);
+      } else {
+        u128 an, o, m;
+        const uint32_t n = compact_upto(cl, nc, w, rank_of(w[cut.id], (uint32_t)cut.id), L[1], an, o, m, sh);
+        pick = descend<true>(L[1], n, an, o, w, x > c_before ? x - c_before : (u128)0, true, L[2], L[3], sh);
+      }
+      if (pick.id >= 0) token = pick.id;
+    }
+  }
+  if (threadIdx.x == 0) a.tokens[s] = token;
+  if (logprobs) {
+    // log-softmax of the raw logits (no temperature, no cuts)
+    double lse = 0.0;
+    for (int c = 0; c < a.chunks; ++c) lse += a.lse_parts[(size_t)r * a.chunks + c];
+    const double log_sum = log(lse);
+    if (threadIdx.x == 0) a.logprob[s] = ((double)lg[token] - best) - log_sum;
+    // The top_logprobs best tokens by (log-probability descending, ID ascending), from
+    // the chunks' candidates (each chunk's best by logit): thread t holds candidate t.
+    const int total_candidates = a.chunks * kCandidates;
+    u64 key = ~0ull;
+    uint32_t id = ~0u;
+    if ((int)threadIdx.x < total_candidates) {
+      const uint32_t c = a.candidates[(size_t)r * total_candidates + threadIdx.x];
+      if (c < V) {
+        id = c;
+        key = descending_key(((double)lg[c] - best) - log_sum);
+      }
+    }
+    const uint32_t rounds = min(p.top_logprobs, min(5u, V));
+    for (uint32_t q = 0; q < rounds; ++q) {
+      u64 bk2 = key;
+      uint32_t bi = id;
+      block_min_pair<kWaves>(bk2, bi, sh.red);
+      if (key == bk2 && id == bi) {
+        key = ~0ull;
+        id = ~0u;
+      }
+      if (threadIdx.x == 0 && bi < V) {
+        a.top_ids[(size_t)s * 5 + q] = (int32_t)bi;
+        a.top_values[(size_t)s * 5 + q] = ((double)lg[bi] - best) - log_sum;
+      }
+    }
   }
 }
 
 }  // namespace
 
-void launch_sample(hipStream_t stream, const SampleArgs& a, int blocks) {
-  if (a.rows <= 0 || blocks <= 0) return;
-  observed("sample_kernel", [&] { sample_kernel<<<std::min(a.rows, blocks), kThreads, 0, stream>>>(a); });
+void launch_sample(hipStream_t stream, const SampleArgs& a) {
+  if (a.rows <= 0 || a.group_rows <= 0) return;
+  if (a.chunks * kCandidates > kThreads) fail(HLLM_INTERNAL, "too many sampling chunks");
+  for (int row0 = 0; row0 < a.rows; row0 += a.group_rows) {
+    const int n = std::min(a.group_rows, a.rows - row0);
+    observed("sample_histogram_kernel",
+             [&] { sample_histogram_kernel<<<dim3(a.chunks, n), kPassThreads, 0, stream>>>(a, row0); });
+    observed("sample_scatter_kernel",
+             [&] { sample_scatter_kernel<<<dim3(a.chunks, n), kPassThreads, 0, stream>>>(a, row0); });
+    observed("sample_select_kernel", [&] { sample_select_kernel<<<n, kThreads, 0, stream>>>(a, row0); });
+  }
 }
 
 }  // namespace hllm_rocm

@@ -210,9 +210,10 @@ class Stage {
   PackOut pack_{};
   PinnedMemory pin_items_, pin_tokens_, pin_out_tokens_, pin_flags_, pin_boundary_;
   // sampler: per-row options, outputs [logprob: items][top values: items * 5][top IDs: items * 5]
-  DeviceMemory sample_params_, sample_out_, sample_weights_, sample_lists_;
+  DeviceMemory sample_params_, sample_out_, sample_weights_, sample_lists_, sample_buckets_, sample_hist_,
+      sample_lse_, sample_sorted_, sample_cursor_, sample_candidates_;
   PinnedMemory pin_sample_params_, pin_sample_out_;
-  int sample_blocks_ = 0;
+  int sample_blocks_ = 0, sample_chunks_ = 1;
 
   // Passes whose shape (items, rows, sampled rows, sampler, attention work items) repeats
   // can be replayed from a captured HIP graph (off by default: on MI355X the replay saves
@@ -393,10 +394,19 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     argmax_val_.allocate(items_max_ * kArgmaxParts * sizeof(float), "argmax");
     argmax_idx_.allocate(items_max_ * kArgmaxParts * sizeof(int32_t), "argmax");
     sample_blocks_ = (int)std::min<uint64_t>(items_max_, kSampleBlocks);
+    sample_chunks_ = std::max(1, std::min(32, 4 * cus_ / sample_blocks_));
     sample_params_.allocate(items_max_ * sizeof(SampleParams), "sampling");
     sample_out_.allocate(items_max_ * (6 * sizeof(double) + 5 * sizeof(int32_t)), "sampling");
     sample_weights_.allocate((size_t)sample_blocks_ * V_ * sizeof(double), "sampling workspace");
-    sample_lists_.allocate((size_t)sample_blocks_ * 3 * V_ * sizeof(uint32_t), "sampling workspace");
+    sample_buckets_.allocate((size_t)sample_blocks_ * sample_bucket_stride(V_), "sampling workspace");
+    sample_lists_.allocate((size_t)sample_blocks_ * 4 * V_ * sizeof(uint32_t), "sampling workspace");
+    sample_hist_.allocate((size_t)sample_blocks_ * 256 * 3 * sizeof(uint64_t), "sampling workspace");
+    sample_lse_.allocate((size_t)sample_blocks_ * sample_chunks_ * sizeof(double), "sampling workspace");
+    sample_sorted_.allocate((size_t)sample_blocks_ * V_ * sizeof(uint32_t), "sampling workspace");
+    sample_cursor_.allocate((size_t)sample_blocks_ * 256 * sizeof(uint32_t), "sampling workspace");
+    sample_candidates_.allocate((size_t)sample_blocks_ * sample_chunks_ * 8 * sizeof(uint32_t), "sampling workspace");
+    HIP_CHECK(hipMemsetAsync(sample_hist_.ptr, 0, sample_hist_.bytes, stream_));
+    HIP_CHECK(hipMemsetAsync(sample_cursor_.ptr, 0, sample_cursor_.bytes, stream_));
   }
   tokens_.allocate(items_max_ * sizeof(int32_t), "tokens");
   flags_.allocate(sizeof(int32_t), "flags");
@@ -1197,8 +1207,17 @@ void Stage::submit(const hllm_rocm_pass& pass) {
           sa.top_values = sa.logprob + items_max_;
           sa.top_ids = reinterpret_cast<int32_t*>(sa.top_values + 5 * items_max_);
           sa.weights = sample_weights_.as<double>();
+          sa.buckets = sample_buckets_.as<uint8_t>();
+          sa.bucket_stride = sample_bucket_stride(V_);
           sa.lists = sample_lists_.as<uint32_t>();
-          timed("sample", (uint64_t)S * V_ * 4, 0.0, [&] { launch_sample(stream_, sa, sample_blocks_); });
+          sa.hist = sample_hist_.as<uint64_t>();
+          sa.lse_parts = sample_lse_.as<double>();
+          sa.sorted = sample_sorted_.as<uint32_t>();
+          sa.cursor = sample_cursor_.as<uint32_t>();
+          sa.candidates = sample_candidates_.as<uint32_t>();
+          sa.group_rows = sample_blocks_;
+          sa.chunks = sample_chunks_;
+          timed("sample", (uint64_t)S * V_ * 4, 0.0, [&] { launch_sample(stream_, sa); });
           HIP_CHECK(hipMemcpyAsync(pin_sample_out_.ptr, sample_out_.ptr, sample_out_.bytes, hipMemcpyDeviceToHost,
                                    stream_));
         }
@@ -1356,7 +1375,11 @@ void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t 
   } st;
   HIP_CHECK(hipStreamCreate(&st.s));
   const int blocks = (int)std::min<uint64_t>(rows, kSampleBlocks);
-  DeviceMemory d_logits, d_rows, d_tokens, d_flags, d_val, d_idx, d_params, d_out, d_w, d_lists;
+  DeviceMemory d_logits, d_rows, d_tokens, d_flags, d_val, d_idx, d_params, d_out, d_w, d_lists, d_buckets, d_hist,
+      d_lse, d_sorted, d_cursor, d_candidates;
+  int cus = 256;
+  HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  const int chunks = std::max(1, std::min(32, 4 * cus / blocks));
   d_logits.allocate(rows * V * sizeof(float), "logits");
   d_rows.allocate(sizeof(int32_t), "sampling");
   d_tokens.allocate(rows * sizeof(int32_t), "sampling");
@@ -1366,7 +1389,15 @@ void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t 
   d_params.allocate(rows * sizeof(SampleParams), "sampling");
   d_out.allocate(rows * (6 * sizeof(double) + 5 * sizeof(int32_t)), "sampling");
   d_w.allocate((size_t)blocks * V * sizeof(double), "sampling workspace");
-  d_lists.allocate((size_t)blocks * 3 * V * sizeof(uint32_t), "sampling workspace");
+  d_lists.allocate((size_t)blocks * 4 * V * sizeof(uint32_t), "sampling workspace");
+  d_buckets.allocate((size_t)blocks * sample_bucket_stride(V), "sampling workspace");
+  d_hist.allocate((size_t)blocks * 256 * 3 * sizeof(uint64_t), "sampling workspace");
+  d_lse.allocate((size_t)blocks * chunks * sizeof(double), "sampling workspace");
+  d_sorted.allocate((size_t)blocks * V * sizeof(uint32_t), "sampling workspace");
+  d_cursor.allocate((size_t)blocks * 256 * sizeof(uint32_t), "sampling workspace");
+  d_candidates.allocate((size_t)blocks * chunks * 8 * sizeof(uint32_t), "sampling workspace");
+  HIP_CHECK(hipMemsetAsync(d_hist.ptr, 0, d_hist.bytes, st.s));
+  HIP_CHECK(hipMemsetAsync(d_cursor.ptr, 0, d_cursor.bytes, st.s));
   const int32_t count = (int32_t)rows;
   HIP_CHECK(hipMemcpyAsync(d_logits.ptr, logits, d_logits.bytes, hipMemcpyHostToDevice, st.s));
   HIP_CHECK(hipMemcpyAsync(d_rows.ptr, &count, sizeof(count), hipMemcpyHostToDevice, st.s));
@@ -1384,8 +1415,17 @@ void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t 
   sa.top_values = sa.logprob + rows;
   sa.top_ids = reinterpret_cast<int32_t*>(sa.top_values + 5 * rows);
   sa.weights = d_w.as<double>();
+  sa.buckets = d_buckets.as<uint8_t>();
+  sa.bucket_stride = sample_bucket_stride(V);
   sa.lists = d_lists.as<uint32_t>();
-  launch_sample(st.s, sa, blocks);
+  sa.hist = d_hist.as<uint64_t>();
+  sa.lse_parts = d_lse.as<double>();
+  sa.sorted = d_sorted.as<uint32_t>();
+  sa.cursor = d_cursor.as<uint32_t>();
+  sa.candidates = d_candidates.as<uint32_t>();
+  sa.group_rows = blocks;
+  sa.chunks = chunks;
+  launch_sample(st.s, sa);
   HIP_CHECK(hipGetLastError());
   std::vector<int32_t> t(rows);
   std::vector<unsigned char> out(d_out.bytes);
