@@ -37,7 +37,7 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
     gemm_kernel(GemmArgs a, int n_tiles, int tiles, int tiles_padded) {
   constexpr int BM = 16 * MF * WM, BN = 16 * NF * WN, NT = 64 * WM * WN * WK;
   constexpr int LDT = BN + 4;  // padded LDS row (floats)
-  extern __shared__ float lds[];  // [BM][LDT] + flag
+  extern __shared__ float lds[];  // [WK][BM][LDT] + flag
   const int M = a.device_m ? *a.device_m : a.M;
   // Block order: id = split * tiles_padded + tile (tiles_padded % 8 == 0), so every split
   // of a tile has the same id modulo 8, i.e. runs on the same XCD.
@@ -133,38 +133,43 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   for (int s = 0; s < P; ++s)
     if (base + s < steps) compute(s);
 
-  // Per-wave partial tiles -> one LDS tile, the K-interleaved waves adding in turn
-  // (fixed order, so the sum is deterministic).
+  // Per-wave partial tiles -> one LDS tile. Each K-wave stores its tile in an LDS area of
+  // its own, then every thread sums its elements over the areas in wave order (the order
+  // of a sequential accumulation, so the sum is deterministic) into area 0.
+  {
+    float* mine = lds + (size_t)wk * BM * LDT;
 #pragma unroll
-  for (int turn = 0; turn < WK; ++turn) {
-    if (wk == turn) {
+    for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int i = 0; i < MF; ++i)
-#pragma unroll
-        for (int j = 0; j < NF; ++j) {
-          floatx4 v = acc[i][j];
-          if constexpr (PREC >= kSplitA) {
-            v[0] += acc2[i][j][0] * kLoUnscale;
-            v[1] += acc2[i][j][1] * kLoUnscale;
-            v[2] += acc2[i][j][2] * kLoUnscale;
-            v[3] += acc2[i][j][3] * kLoUnscale;
-          }
-          const int m = (wm * MF + i) * 16 + (lane & 15);
-          const int n = (wn * NF + j) * 16 + (lane >> 4) * 4;
-          floatx4* dst = reinterpret_cast<floatx4*>(lds + m * LDT + n);
-          if (turn == 0) {
-            *dst = v;
-          } else {
-            floatx4 s = *dst;
-            s[0] += v[0];
-            s[1] += v[1];
-            s[2] += v[2];
-            s[3] += v[3];
-            *dst = s;
-          }
+      for (int j = 0; j < NF; ++j) {
+        floatx4 v = acc[i][j];
+        if constexpr (PREC >= kSplitA) {
+          v[0] += acc2[i][j][0] * kLoUnscale;
+          v[1] += acc2[i][j][1] * kLoUnscale;
+          v[2] += acc2[i][j][2] * kLoUnscale;
+          v[3] += acc2[i][j][3] * kLoUnscale;
         }
-    }
+        const int m = (wm * MF + i) * 16 + (lane & 15);
+        const int n = (wn * NF + j) * 16 + (lane >> 4) * 4;
+        *reinterpret_cast<floatx4*>(mine + m * LDT + n) = v;
+      }
     __syncthreads();
+    if constexpr (WK > 1) {
+      for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
+        const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
+        floatx4 sum = *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
+#pragma unroll
+        for (int t = 1; t < WK; ++t) {
+          const floatx4 x = *reinterpret_cast<const floatx4*>(lds + (size_t)t * BM * LDT + m * LDT + n);
+          sum[0] += x[0];
+          sum[1] += x[1];
+          sum[2] += x[2];
+          sum[3] += x[3];
+        }
+        *reinterpret_cast<floatx4*>(lds + m * LDT + n) = sum;
+      }
+      __syncthreads();
+    }
   }
 
   if (a.ksplit > 1 && a.defer_reduce) {
@@ -576,6 +581,237 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a, int n_tile
   }
 }
 
+// Pipelined variant for passes of many rows (F16 execution): both operands go from HBM/L2
+// straight into LDS with direct-to-LDS loads (no register staging), in a ring of six
+// one-k-step stages, so a stage's loads have four stages of MFMA work to land. Tile BM 128
+// x BN 256; the four waves are 2 x 2, each computing 64 rows x 128 features from LDS
+// fragments (4 activation and 8 weight fragments per k-step). Every wave copies 6 of a
+// k-step's 24 fragments (1 KiB each: one 16-byte load per lane), waits for its own copies
+// of the next stage, and meets the others at a barrier; it then reads that stage into one
+// register set while the MFMAs consume the other. The copies are issued from inline
+// assembly so that the compiler, which cannot tell the stages apart, does not drain every
+// copy in flight before each LDS read; the waits on them are written out by hand.
+namespace dma {
+constexpr int BM = 128, BN = 256, NS = 6;
+constexpr int FRAGS = BM / 16 + BN / 16;          // 24 fragments per k-step
+constexpr int STAGE_BYTES = FRAGS * 1024;         // 24 KiB
+constexpr int LDS_BYTES = NS * STAGE_BYTES;       // 144 KiB
+constexpr int PER_WAVE = FRAGS / 4;               // copies per wave per stage
+}  // namespace dma
+
+// One 16-byte copy per lane from sbase + voffset to LDS byte m0 + 16 * lane; sbase and
+// the LDS offset are uniform over the wave.
+__device__ inline void lds_copy16(const void* sbase, uint32_t voffset, uint32_t lds_byte_offset) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voffset), "s"(sbase),
+               "s"(lds_byte_offset)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// Wait until at most `in_flight` of this wave's copies are outstanding and every LDS read
+// it issued has returned, then meet the other waves.
+template <int in_flight>
+__device__ inline void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(in_flight) : "memory");
+}
+
+__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
+  using namespace dma;
+  extern __shared__ float lds[];
+  const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
+  const int M = a.device_m ? *a.device_m : a.M;
+  const int slots = n_groups * m_tiles * 8;
+  const int split = blockIdx.x / slots;
+  const int r = blockIdx.x - split * slots;
+  const int group_m = r >> 3;
+  const int group = group_m / m_tiles, tile_m = group_m - group * m_tiles;
+  const int tile_n = group * 8 + (r & 7);
+  if (tile_n >= n_tiles || tile_m * BM >= M) return;  // uniform over the workgroup
+  const int tile = tile_m * n_tiles + tile_n;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int KT = (int)(a.Kp >> 5);
+  const int per = (KT + a.ksplit - 1) / a.ksplit;
+  const int kt0 = split * per, kt1 = min(KT, kt0 + per);
+  const int steps = kt1 > kt0 ? kt1 - kt0 : 0;
+  const size_t frag_stride = (size_t)KT * 64;  // half8s between fragment rows
+  const char* X = reinterpret_cast<const char*>(a.x_hi) + (size_t)tile_m * (BM / 16) * frag_stride * 16;
+  const char* W = reinterpret_cast<const char*>(a.w_hi) + (size_t)tile_n * (BN / 16) * frag_stride * 16;
+  const uint32_t lane_bytes = (uint32_t)lane * 16;
+  // Stages come in pairs: an odd count gets one more stage, a copy of the last k-step whose
+  // activations are zeroed in registers before its MFMAs.
+  const int stages = (steps + 1) & ~1;
+  const int kt_last = max(kt0, kt1 - 1);
+  // This wave's copies of stage st into buffer st % NS (the caller keeps st < stages).
+  auto issue = [&](int st) {
+    const uint32_t buf = lds_base + (uint32_t)(st % NS) * STAGE_BYTES;
+    const size_t k = (size_t)min(kt0 + st, kt_last) * 1024;
+#pragma unroll
+    for (int c = 0; c < PER_WAVE; ++c) {
+      const int f = wave * PER_WAVE + c;
+      const char* src = f < BM / 16 ? X + (size_t)f * frag_stride * 16 : W + (size_t)(f - BM / 16) * frag_stride * 16;
+      lds_copy16(src + k, lane_bytes, __builtin_amdgcn_readfirstlane(buf + (uint32_t)f * 1024));
+    }
+  };
+  const half8* ldsh = reinterpret_cast<const half8*>(lds);
+  auto read = [&](int st, half8 (&x)[4], half8 (&w)[8]) {
+    const half8* stage = ldsh + (size_t)(st % NS) * (STAGE_BYTES / 16) + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = stage[(wm * 4 + i) * 64];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) w[n] = stage[(BM / 16 + wn * 8 + n) * 64];
+  };
+
+  floatx4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[i][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto multiply = [&](const half8 (&x)[4], const half8 (&w)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) acc[i][n] = mfma(w[n], x[i], acc[i][n]);
+  };
+
+  // Copies are issued in stage order and only for stages < stages. Before stage st + 1 is
+  // read, the stages issued are 0 .. min(stages, st + NS - 1) - 1; when all of
+  // st + 1 .. st + NS - 2 exist, NS - 3 stages may stay in flight, otherwise none.
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < stages) issue(st);
+  if (stages >= NS - 1)
+    stage_barrier<(NS - 2) * PER_WAVE>();
+  else
+    stage_barrier<0>();
+  half8 xa[4], wa[8], xb[4], wb[8];
+  read(0, xa, wa);
+  auto advance = [&](int st) {  // stage st + 1 becomes readable; stage st + NS - 1 is issued
+    if (st + NS - 2 < stages)
+      stage_barrier<(NS - 3) * PER_WAVE>();
+    else
+      stage_barrier<0>();
+    if (st + NS - 1 < stages) issue(st + NS - 1);
+  };
+  for (int st = 0; st < stages; st += 2) {
+    advance(st);
+    read(st + 1, xb, wb);
+    multiply(xa, wa);
+    advance(st + 1);
+    read(st + 2, xa, wa);  // past the last stage this reads a buffer that is never used
+    if (st + 1 >= steps) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xb[i] = half8{};
+    }
+    multiply(xb, wb);
+  }
+  // Drain the copies still in flight before the workgroup's LDS can be reused.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Lane (q, t) of accumulator (i, n) holds row 64 wm + 16 i + t, features 128 wn + 16 n +
+  // 4 q .. + 3 of the tile.
+  const int q4 = (lane >> 4) * 4, t16 = lane & 15;
+  const int row0 = tile_m * BM + wm * 64, col0 = tile_n * BN + wn * 128;
+  if (a.ksplit > 1 && a.defer_reduce) {
+    float* ws = a.workspace + (size_t)split * a.M * a.N;
+    const bool vec = (a.N & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + i * 16 + t16;
+      if (row >= M) continue;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const int col = col0 + n * 16 + q4;
+        float* dst = ws + (size_t)row * a.N + col;
+        if (vec && col + 3 < a.N) {
+          *reinterpret_cast<floatx4*>(dst) = acc[i][n];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (col + t < a.N) dst[t] = acc[i][n][t];
+        }
+      }
+    }
+    return;
+  }
+  if (a.ksplit > 1) {
+    // Partial tile of this K split (row-major BM x BN), summed by gemm_reduce_kernel.
+    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+        *reinterpret_cast<floatx4*>(ws + (wm * 64 + i * 16 + t16) * BN + wn * 128 + n * 16 + q4) = acc[i][n];
+    return;
+  }
+  if (a.epilogue == kEpiSwiglu) {
+    // The wave's 128 features are two 64-wide groups: 32 gate features (fragments 4g,
+    // 4g + 1), then the 32 matching up features (fragments 4g + 2, 4g + 3).
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      const uint64_t g = (uint64_t)col0 / 64 + gq;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + i * 16 + t16;
+        if (row >= M) continue;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint64_t col = g * 32 + h * 16 + q4;
+          if (col >= a.out_cols_padded) continue;
+          const floatx4 gate = acc[i][4 * gq + h], up = acc[i][4 * gq + 2 + h];
+          half4 vh, vl;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float y = silu_mul(gate[t], up[t]);
+            vh[t] = to_half(y);
+            vl[t] = to_half((y - (float)vh[t]) * kLoScale);
+          }
+          const uint64_t at = flayout_index(row, col, a.out_cols_padded);
+          *reinterpret_cast<half4*>(a.out_hi + at) = vh;
+          if (a.out_lo) *reinterpret_cast<half4*>(a.out_lo + at) = vl;
+        }
+      }
+    }
+    return;
+  }
+  const bool vec = (a.N & 3) == 0 && (a.ldo & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + i * 16 + t16;
+    if (row >= M) continue;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int col = col0 + n * 16 + q4;
+      if (col >= a.N) continue;
+      float* out = a.out + (size_t)row * a.ldo + col;
+      const floatx4 v = acc[i][n];
+      if (vec && col + 3 < a.N) {
+        floatx4* o4 = reinterpret_cast<floatx4*>(out);
+        if (a.epilogue == kEpiResidual) {
+          floatx4 s4 = *o4;
+          s4[0] += v[0];
+          s4[1] += v[1];
+          s4[2] += v[2];
+          s4[3] += v[3];
+          *o4 = s4;
+        } else {
+          *o4 = v;
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (col + t >= a.N) continue;
+          if (a.epilogue == kEpiResidual)
+            out[t] += v[t];
+          else
+            out[t] = v[t];
+        }
+      }
+    }
+  }
+}
+
 template <int MF, int NF, int WM, int WN, int WK, int P, int PREC>
 void run(dim3 grid, int threads, size_t lds, hipStream_t stream, const GemmArgs& a, int n_tiles,
          int tiles, int tiles_padded) {
@@ -618,7 +854,7 @@ int launch_config(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int 
   const int tiles_padded = (tiles + kXcds - 1) / kXcds * kXcds;
   ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
   a.ksplit = ksplit;
-  const size_t lds = ((size_t)BM * (BN + 4) + 4) * sizeof(float);
+  const size_t lds = ((size_t)WK * BM * (BN + 4) + 4) * sizeof(float);
   dim3 grid(tiles_padded * ksplit, 1, 1);
   switch (prec) {
     case kF16:
@@ -694,6 +930,36 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
   return 0;
 }
 
+int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas, int forced_ksplit) {
+  using namespace dma;
+  if (prec != kF16) return launch_xlds<8, 4, 4, 2>(stream, a, prec, rows_bound, target_ctas, forced_ksplit);
+  const int n_tiles = (a.N + BN - 1) / BN;
+  const int m_tiles = (rows_bound + BM - 1) / BM;
+  const int n_groups = (n_tiles + kXcds - 1) / kXcds;
+  const int tiles = n_tiles * m_tiles;
+  const int KT = (int)(a.Kp >> 5);
+  if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
+  if ((uint64_t)m_tiles * BM > a.x_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the activation padding");
+  int ksplit = forced_ksplit > 0 ? forced_ksplit : (tiles < target_ctas ? (target_ctas + tiles - 1) / tiles : 1);
+  ksplit = std::min(ksplit, std::max(1, KT / (2 * NS)));  // at least two rings of k-steps per split
+  ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
+  a.ksplit = ksplit;
+  static const bool configured = [] {
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+    return true;
+  }();
+  (void)configured;
+  const dim3 grid((unsigned)(ksplit * n_groups * m_tiles * kXcds));
+  observed("gemm_dma_kernel", [&] { gemm_dma_kernel<<<grid, 256, LDS_BYTES, stream>>>(a, n_tiles, m_tiles, n_groups); });
+  if (ksplit > 1 && a.defer_reduce) return ksplit;
+  if (ksplit > 1) {
+    const int64_t threads = (int64_t)tiles * BM * BN / 8;
+    observed(kernel_name<BM, BN>("gemm_reduce_kernel"), [&] { gemm_reduce_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a, n_tiles, tiles); });
+  }
+  return 0;
+}
+
 }  // namespace
 
 
@@ -742,6 +1008,8 @@ int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int r
       break;
     case 13:  // BM 192 x BN 256, chunks of 2, ring of 2 (accumulators in AGPRs, one wave per SIMD)
       return launch_xlds<12, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
+    case 14:  // BM 128 x BN 256, both operands copied to LDS, six one-k-step stages (F16 execution)
+      return launch_dma(stream, args, prec, rows_bound, cus, forced_ksplit);
     default:
       return launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
       break;
