@@ -29,7 +29,7 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
            "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
-           "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats")
+           "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config")
 
 
 class StageError(RuntimeError):
@@ -120,6 +120,7 @@ def library() -> C.CDLL:
     L.hllm_rocm_stage_profile_records.argtypes = [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64)]
     L.hllm_rocm_stage_set_graphs.argtypes = [vp, u32]
     L.hllm_rocm_stage_graph_stats.argtypes = [vp, C.POINTER(u64), C.POINTER(u64)]
+    L.hllm_rocm_set_gemm_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
     L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
@@ -341,6 +342,14 @@ def sample_logits(logits, options, device: int = 0):
                                              _ptr(tokens, C.c_uint64), _ptr(logprobs, C.c_double),
                                              _ptr(top_ids, C.c_uint64), _ptr(top_lp, C.c_double)))
     return tokens, logprobs, top_ids, top_lp
+
+
+def set_gemm_config(config: int) -> int:
+    """Process-wide projection GEMM configuration override (-1: the choice by shape);
+    returns the previous value."""
+    prev = C.c_int32(0)
+    check(library().hllm_rocm_set_gemm_config(config, C.byref(prev)))
+    return prev.value
 
 
 def item(sequence: int, query_tokens: int, first_position: int, sample: bool = True,

@@ -19,6 +19,7 @@
 #include "gemm.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 
 namespace hllm_rocm {
@@ -582,21 +583,24 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a, int n_tile
 }
 
 // Pipelined variant for passes of many rows (F16 execution): both operands go from HBM/L2
-// straight into LDS with direct-to-LDS loads (no register staging), in a ring of six
-// one-k-step stages, so a stage's loads have four stages of MFMA work to land. Tile BM 128
-// x BN 256; the four waves are 2 x 2, each computing 64 rows x 128 features from LDS
-// fragments (4 activation and 8 weight fragments per k-step). Every wave copies 6 of a
-// k-step's 24 fragments (1 KiB each: one 16-byte load per lane), waits for its own copies
-// of the next stage, and meets the others at a barrier; it then reads that stage into one
-// register set while the MFMAs consume the other. The copies are issued from inline
-// assembly so that the compiler, which cannot tell the stages apart, does not drain every
-// copy in flight before each LDS read; the waits on them are written out by hand.
+// straight into LDS with direct-to-LDS loads (no register staging) through a ring of
+// one-k-step buffers. Tile BM (128 or 256) x 256 features; WM x WN waves, each computing
+// BM / WM rows x 256 / WN features from LDS fragments. Every wave copies its share of a
+// k-step's fragments (1 KiB each: one 16-byte load per lane). The waves meet at a barrier
+// every two k-steps; a wave then reads the next k-step into one register set while its
+// MFMAs consume the other. The copies are issued from inline assembly so that the compiler,
+// which cannot tell the buffers apart, does not drain every copy in flight before each LDS
+// read; the waits on them are written out by hand.
 namespace dma {
-constexpr int BM = 128, BN = 256, NS = 6;
-constexpr int FRAGS = BM / 16 + BN / 16;          // 24 fragments per k-step
-constexpr int STAGE_BYTES = FRAGS * 1024;         // 24 KiB
-constexpr int LDS_BYTES = NS * STAGE_BYTES;       // 144 KiB
-constexpr int PER_WAVE = FRAGS / 4;               // copies per wave per stage
+constexpr int BN = 256;
+constexpr int kLdsMax = 160 * 1024;
+template <int BM>
+struct Ring {
+  static constexpr int kFrags = BM / 16 + BN / 16;  // fragments per k-step
+  static constexpr int kBytes = kFrags * 1024;      // one buffer
+  static constexpr int kBuffers = kLdsMax / kBytes > 6 ? 6 : kLdsMax / kBytes;
+  static constexpr int kLds = kBuffers * kBytes;
+};
 }  // namespace dma
 
 // One 16-byte copy per lane from sbase + voffset to LDS byte m0 + 16 * lane; sbase and
@@ -610,15 +614,33 @@ __device__ inline void lds_copy16(const void* sbase, uint32_t voffset, uint32_t 
 #pragma clang diagnostic pop
 }
 
-// Wait until at most `in_flight` of this wave's copies are outstanding and every LDS read
-// it issued has returned, then meet the other waves.
-template <int in_flight>
-__device__ inline void stage_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(in_flight) : "memory");
+// s_waitcnt with the given vector-memory and LDS counts (expcnt left open). Issued through
+// the builtin so that the compiler knows which of its own LDS reads have completed.
+template <int vm, int lgkm>
+__device__ inline void wait_counts() {
+  static_assert(vm >= 0 && vm < 64 && lgkm >= 0 && lgkm < 16, "s_waitcnt field range");
+  __builtin_amdgcn_s_waitcnt((vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (lgkm << 8));
 }
 
-__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
+// Wait until at most `in_flight` of this wave's copies are outstanding and all but its
+// last `reads` LDS reads have returned, then meet the other waves.
+template <int in_flight, int reads>
+__device__ inline void stage_barrier() {
+  wait_counts<in_flight, reads>();
+  asm volatile("s_barrier" ::: "memory");
+}
+
+template <int BM, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
+    gemm_dma_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
   using namespace dma;
+  using R = Ring<BM>;
+  constexpr int NS = R::kBuffers;
+  constexpr int MF = BM / 16 / WM;                    // activation fragments per wave
+  constexpr int NF = BN / 16 / WN;                    // weight fragments per wave
+  constexpr int kPer = R::kFrags / (WM * WN);         // copies per wave per k-step
+  constexpr int kReads = MF + NF;                     // LDS reads per wave per k-step
+  static_assert(R::kFrags % (WM * WN) == 0 && NS >= 5 && kReads <= 15, "DMA GEMM shape");
   extern __shared__ float lds[];
   const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
   const int M = a.device_m ? *a.device_m : a.M;
@@ -631,7 +653,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tile
   if (tile_n >= n_tiles || tile_m * BM >= M) return;  // uniform over the workgroup
   const int tile = tile_m * n_tiles + tile_n;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int KT = (int)(a.Kp >> 5);
   const int per = (KT + a.ksplit - 1) / a.ksplit;
   const int kt0 = split * per, kt1 = min(KT, kt0 + per);
@@ -640,88 +662,98 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tile
   const char* X = reinterpret_cast<const char*>(a.x_hi) + (size_t)tile_m * (BM / 16) * frag_stride * 16;
   const char* W = reinterpret_cast<const char*>(a.w_hi) + (size_t)tile_n * (BN / 16) * frag_stride * 16;
   const uint32_t lane_bytes = (uint32_t)lane * 16;
-  // Stages come in pairs: an odd count gets one more stage, a copy of the last k-step whose
+  // K-steps come in pairs: an odd count gets one more, a copy of the last k-step whose
   // activations are zeroed in registers before its MFMAs.
   const int stages = (steps + 1) & ~1;
   const int kt_last = max(kt0, kt1 - 1);
-  // This wave's copies of stage st into buffer st % NS (the caller keeps st < stages).
+  // This wave's copies of k-step st into buffer st % NS (the caller keeps st < stages).
   auto issue = [&](int st) {
-    const uint32_t buf = lds_base + (uint32_t)(st % NS) * STAGE_BYTES;
+    const uint32_t buf = lds_base + (uint32_t)(st % NS) * R::kBytes;
     const size_t k = (size_t)min(kt0 + st, kt_last) * 1024;
 #pragma unroll
-    for (int c = 0; c < PER_WAVE; ++c) {
-      const int f = wave * PER_WAVE + c;
+    for (int c = 0; c < kPer; ++c) {
+      const int f = wave * kPer + c;
       const char* src = f < BM / 16 ? X + (size_t)f * frag_stride * 16 : W + (size_t)(f - BM / 16) * frag_stride * 16;
       lds_copy16(src + k, lane_bytes, __builtin_amdgcn_readfirstlane(buf + (uint32_t)f * 1024));
     }
   };
   const half8* ldsh = reinterpret_cast<const half8*>(lds);
-  auto read = [&](int st, half8 (&x)[4], half8 (&w)[8]) {
-    const half8* stage = ldsh + (size_t)(st % NS) * (STAGE_BYTES / 16) + lane;
+  auto read = [&](int st, half8 (&x)[MF], half8 (&w)[NF]) {
+    const half8* stage = ldsh + (size_t)(st % NS) * (R::kBytes / 16) + lane;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = stage[(wm * 4 + i) * 64];
+    for (int i = 0; i < MF; ++i) x[i] = stage[(wm * MF + i) * 64];
 #pragma unroll
-    for (int n = 0; n < 8; ++n) w[n] = stage[(BM / 16 + wn * 8 + n) * 64];
+    for (int n = 0; n < NF; ++n) w[n] = stage[(BM / 16 + wn * NF + n) * 64];
   };
 
-  floatx4 acc[4][8];
+  floatx4 acc[MF][NF];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MF; ++i)
 #pragma unroll
-    for (int n = 0; n < 8; ++n) acc[i][n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto multiply = [&](const half8 (&x)[4], const half8 (&w)[8]) {
+    for (int n = 0; n < NF; ++n) acc[i][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto multiply = [&](const half8 (&x)[MF], const half8 (&w)[NF]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int n = 0; n < 8; ++n) acc[i][n] = mfma(w[n], x[i], acc[i][n]);
+      for (int n = 0; n < NF; ++n) acc[i][n] = mfma(w[n], x[i], acc[i][n]);
   };
 
-  // Copies are issued in stage order and only for stages < stages. Before stage st + 1 is
-  // read, the stages issued are 0 .. min(stages, st + NS - 1) - 1; when all of
-  // st + 1 .. st + NS - 2 exist, NS - 3 stages may stay in flight, otherwise none.
-  for (int st = 0; st < NS - 1; ++st)
+  // Copies are issued in k-step order and only for k-steps < stages: 0 .. NS - 3 before
+  // the loop, then st + NS - 2 and st + NS - 1 after the barrier at pair st (even), into
+  // the buffers of st - 2 and st - 1. At that barrier k-steps st + 1 and st + 2 must have
+  // landed; when all of st + 3 .. st + NS - 3 were issued, NS - 5 k-steps may stay in
+  // flight, otherwise none. Every LDS read a wave issued has returned before it reaches
+  // the barrier (the last group was issued a half-iteration of MFMAs earlier), so the
+  // refilled buffers are free, and the register sets are complete when their MFMAs start.
+  for (int st = 0; st < NS - 2; ++st)
     if (st < stages) issue(st);
-  if (stages >= NS - 1)
-    stage_barrier<(NS - 2) * PER_WAVE>();
+  if (stages >= NS - 2)
+    stage_barrier<(NS - 3) * kPer, 0>();
   else
-    stage_barrier<0>();
-  half8 xa[4], wa[8], xb[4], wb[8];
+    stage_barrier<0, 0>();
+  half8 xa[MF], wa[NF], xb[MF], wb[NF];
   read(0, xa, wa);
-  auto advance = [&](int st) {  // stage st + 1 becomes readable; stage st + NS - 1 is issued
-    if (st + NS - 2 < stages)
-      stage_barrier<(NS - 3) * PER_WAVE>();
-    else
-      stage_barrier<0>();
-    if (st + NS - 1 < stages) issue(st + NS - 1);
-  };
   for (int st = 0; st < stages; st += 2) {
-    advance(st);
+    wait_counts<63, 0>();  // on both paths below; stated once for the compiler's benefit
+    if (st + NS - 3 < stages)
+      stage_barrier<(NS - 5) * kPer, 0>();
+    else
+      stage_barrier<0, 0>();
+    if (st + NS - 2 < stages) issue(st + NS - 2);
+    if (st + NS - 1 < stages) issue(st + NS - 1);
+    // Each register set is read a whole half-iteration of MFMAs before it is used; the
+    // scheduling barriers keep the compiler from sinking the reads next to their uses, and
+    // the explicit waits (on reads issued that long ago) keep it from waiting on the
+    // reads just issued.
     read(st + 1, xb, wb);
+    __builtin_amdgcn_sched_barrier(0);
     multiply(xa, wa);
-    advance(st + 1);
-    read(st + 2, xa, wa);  // past the last stage this reads a buffer that is never used
+    __builtin_amdgcn_sched_barrier(0);
+    wait_counts<63, 0>();
+    read(st + 2, xa, wa);  // past the last k-step this reads a buffer that is never used
+    __builtin_amdgcn_sched_barrier(0);
     if (st + 1 >= steps) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xb[i] = half8{};
+      for (int i = 0; i < MF; ++i) xb[i] = half8{};
     }
     multiply(xb, wb);
   }
   // Drain the copies still in flight before the workgroup's LDS can be reused.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Lane (q, t) of accumulator (i, n) holds row 64 wm + 16 i + t, features 128 wn + 16 n +
-  // 4 q .. + 3 of the tile.
+  // Lane (q, t) of accumulator (i, n) holds row 16 (MF wm + i) + t, features 16 (NF wn + n)
+  // + 4 q .. + 3 of the tile.
   const int q4 = (lane >> 4) * 4, t16 = lane & 15;
-  const int row0 = tile_m * BM + wm * 64, col0 = tile_n * BN + wn * 128;
+  const int row0 = tile_m * BM + wm * MF * 16, col0 = tile_n * BN + wn * NF * 16;
   if (a.ksplit > 1 && a.defer_reduce) {
     float* ws = a.workspace + (size_t)split * a.M * a.N;
     const bool vec = (a.N & 3) == 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MF; ++i) {
       const int row = row0 + i * 16 + t16;
       if (row >= M) continue;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
+      for (int n = 0; n < NF; ++n) {
         const int col = col0 + n * 16 + q4;
         float* dst = ws + (size_t)row * a.N + col;
         if (vec && col + 3 < a.N) {
@@ -739,20 +771,20 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tile
     // Partial tile of this K split (row-major BM x BN), summed by gemm_reduce_kernel.
     float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int n = 0; n < 8; ++n)
-        *reinterpret_cast<floatx4*>(ws + (wm * 64 + i * 16 + t16) * BN + wn * 128 + n * 16 + q4) = acc[i][n];
+      for (int n = 0; n < NF; ++n)
+        *reinterpret_cast<floatx4*>(ws + (wm * MF * 16 + i * 16 + t16) * BN + wn * NF * 16 + n * 16 + q4) = acc[i][n];
     return;
   }
   if (a.epilogue == kEpiSwiglu) {
-    // The wave's 128 features are two 64-wide groups: 32 gate features (fragments 4g,
-    // 4g + 1), then the 32 matching up features (fragments 4g + 2, 4g + 3).
+    // The wave's features are 64-wide groups: 32 gate features (fragments 4g, 4g + 1),
+    // then the 32 matching up features (fragments 4g + 2, 4g + 3).
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
+    for (int gq = 0; gq < NF / 4; ++gq) {
       const uint64_t g = (uint64_t)col0 / 64 + gq;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < MF; ++i) {
         const int row = row0 + i * 16 + t16;
         if (row >= M) continue;
 #pragma unroll
@@ -777,11 +809,11 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a, int n_tile
   }
   const bool vec = (a.N & 3) == 0 && (a.ldo & 3) == 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < MF; ++i) {
     const int row = row0 + i * 16 + t16;
     if (row >= M) continue;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
+    for (int n = 0; n < NF; ++n) {
       const int col = col0 + n * 16 + q4;
       if (col >= a.N) continue;
       float* out = a.out + (size_t)row * a.ldo + col;
@@ -930,8 +962,10 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
   return 0;
 }
 
+template <int BM, int WM, int WN>
 int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int target_ctas, int forced_ksplit) {
   using namespace dma;
+  using R = Ring<BM>;
   if (prec != kF16) return launch_xlds<8, 4, 4, 2>(stream, a, prec, rows_bound, target_ctas, forced_ksplit);
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
@@ -941,17 +975,19 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
   if ((uint64_t)m_tiles * BM > a.x_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the activation padding");
   int ksplit = forced_ksplit > 0 ? forced_ksplit : (tiles < target_ctas ? (target_ctas + tiles - 1) / tiles : 1);
-  ksplit = std::min(ksplit, std::max(1, KT / (2 * NS)));  // at least two rings of k-steps per split
+  ksplit = std::min(ksplit, std::max(1, KT / (2 * R::kBuffers)));  // at least two rings of k-steps per split
   ksplit = fit_ksplit(a, ksplit, tiles, (size_t)BM * BN);
   a.ksplit = ksplit;
   static const bool configured = [] {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_kernel<BM, WM, WN>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, R::kLds));
     return true;
   }();
   (void)configured;
   const dim3 grid((unsigned)(ksplit * n_groups * m_tiles * kXcds));
-  observed("gemm_dma_kernel", [&] { gemm_dma_kernel<<<grid, 256, LDS_BYTES, stream>>>(a, n_tiles, m_tiles, n_groups); });
+  observed(kernel_name<BM, WM, WN>("gemm_dma_kernel"), [&] {
+    gemm_dma_kernel<BM, WM, WN><<<grid, 64 * WM * WN, R::kLds, stream>>>(a, n_tiles, m_tiles, n_groups);
+  });
   if (ksplit > 1 && a.defer_reduce) return ksplit;
   if (ksplit > 1) {
     const int64_t threads = (int64_t)tiles * BM * BN / 8;
@@ -1008,8 +1044,12 @@ int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int r
       break;
     case 13:  // BM 192 x BN 256, chunks of 2, ring of 2 (accumulators in AGPRs, one wave per SIMD)
       return launch_xlds<12, 4, 2, 2>(stream, args, prec, rows_bound, 2 * cus, forced_ksplit);
-    case 14:  // BM 128 x BN 256, both operands copied to LDS, six one-k-step stages (F16 execution)
-      return launch_dma(stream, args, prec, rows_bound, cus, forced_ksplit);
+    case 14:  // BM 128 x BN 256, both operands copied to LDS (F16 execution), 2 x 2 waves
+      return launch_dma<128, 2, 2>(stream, args, prec, rows_bound, cus, forced_ksplit);
+    case 15:  // as 14 with 2 x 4 waves (two per SIMD), each 64 rows x 64 features
+      return launch_dma<128, 2, 4>(stream, args, prec, rows_bound, cus, forced_ksplit);
+    case 16:  // BM 256 x BN 256, 2 x 4 waves, each 128 rows x 64 features
+      return launch_dma<256, 2, 4>(stream, args, prec, rows_bound, cus, forced_ksplit);
     default:
       return launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
       break;
@@ -1028,8 +1068,9 @@ struct Choice {
 //  - up to 64 rows: the register-streaming decode kernels (BM 16/32/64), except for very
 //    wide outputs (gate+up, LM head) with more than 32 rows, where staging the activations
 //    in LDS once per 256-feature tile wins;
-//  - more rows: the activation-staged kernel, BM 64, or BM 128 from 384 rows (and for
-//    wide outputs from 192 rows).
+//  - more rows: the activation-staged kernel, BM 64, or BM 128 from 384 rows; wide outputs
+//    from 192 to 768 rows use the kernels that copy both operands to LDS (BM 128 below
+//    448 rows, BM 256 from there), and BM 128 activation-staged tiles beyond.
 // K is split while there are few output tiles. When the consumer sums the partials
 // (`deferred`) a split costs one partial write, so about 220-280 workgroups are targeted;
 // otherwise a reduce kernel reads every partial back, so splits stop at about 200
@@ -1042,6 +1083,11 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred) {
     const int tiles = (n + 63) / 64;
     const int cap = std::max(1, (int)(kp >> 5) / 8);  // at least two k-steps per K-wave
     return {config, deferred ? std::min(rounded(220.0 / tiles), cap) : 0};
+  }
+  if (wide && !deferred && rows >= 192 && rows <= 768) {
+    // Both operands copied to LDS: 128-row tiles with eight waves up to 447 rows, 256-row
+    // tiles from 448.
+    return {rows < 448 ? 15 : 16, 1};
   }
   const int bm = rows >= 384 || (wide && rows >= 192) ? 128 : 64;
   const int config = bm == 128 ? 9 : 12;
@@ -1060,13 +1106,22 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred) {
 
 }  // namespace
 
-int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
-  if (rows_bound <= 0) return 0;
-  static const int forced = [] {
+namespace {
+std::atomic<int>& forced_config() {
+  static std::atomic<int> forced{[] {
     const char* v = std::getenv("HLLM_ROCM_GEMM_CONFIG");
     return v ? std::atoi(v) : -1;
-  }();
+  }()};
+  return forced;
+}
+}  // namespace
+
+int set_forced_gemm_config(int config) { return forced_config().exchange(config); }
+
+int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
+  if (rows_bound <= 0) return 0;
   Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0);
+  const int forced = forced_config().load(std::memory_order_relaxed);
   if (forced >= 0) c = {forced, 0};
   return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }

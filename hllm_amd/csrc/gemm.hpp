@@ -45,5 +45,10 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
 // An explicit configuration of the table in gemm.hip (tuning), optionally forcing the K split.
 int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
                         int config, int forced_ksplit);
+// Highest configuration id of the table.
+constexpr int kGemmConfigs = 16;
+// Process-wide override of the configuration choice for every later launch_gemm (-1: the
+// choice by shape; initially HLLM_ROCM_GEMM_CONFIG when set). Returns the previous value.
+int set_forced_gemm_config(int config);
 
 }  // namespace hllm_rocm

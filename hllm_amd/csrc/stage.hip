@@ -1592,6 +1592,15 @@ hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captur
   return guarded([&] { impl(stage).graph_stats(captured, replayed); });
 }
 
+hllm_status hllm_rocm_set_gemm_config(int32_t config, int32_t* previous) {
+  return guarded([&] {
+    if (config < -1 || config > hllm_rocm::kGemmConfigs)
+      hllm_rocm::fail(HLLM_INVALID_REQUEST, "GEMM configuration out of range");
+    const int old = hllm_rocm::set_forced_gemm_config(config);
+    if (previous) *previous = old;
+  });
+}
+
 hllm_status hllm_rocm_stage_last_layout(hllm_rocm_stage* stage, uint32_t items, uint32_t rows,
                                         int32_t* cu_seqlens, int32_t* row_positions, int32_t* row_slots) {
   return guarded([&] { impl(stage).last_layout(items, rows, cu_seqlens, row_positions, row_slots); });

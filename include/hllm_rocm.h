@@ -188,6 +188,13 @@ hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled)
 hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured,
                                         uint64_t* replayed);
 
+/* Tuning and test hook, process-wide: every later projection GEMM uses configuration
+ * `config` of the kernel table (0 .. 16) instead of the choice by shape; -1 restores the
+ * choice by shape. *previous (may be NULL) receives the value replaced. Results stay within
+ * the execution mode's tolerance for every configuration; no counterpart in the reference.
+ * HLLM_ROCM_GEMM_CONFIG gives the initial value. */
+hllm_status hllm_rocm_set_gemm_config(int32_t config, int32_t* previous);
+
 /* Diagnostics for parity tests, like the reference's traced execution
  * (cpp/include/hllm/cuda/stage.hpp:8-21): the last pass's device-built packing
  * (cu_seqlens [items + 1], per-row positions and KV slots [rows]), a sequence's physical

@@ -67,3 +67,12 @@ def test_calls_without_a_stage_fail_cleanly():
     assert lib.hllm_rocm_stage_finalize(None) == capi.INVALID_REQUEST
     assert b"null" in lib.hllm_rocm_last_error()
     assert lib.hllm_rocm_stage_create(None, None) == capi.INVALID_REQUEST
+
+
+def test_gemm_configuration_hook_validates_and_restores():
+    previous = capi.set_gemm_config(-1)
+    assert capi.set_gemm_config(previous) == -1
+    for bad in (-2, 17):
+        with pytest.raises(capi.StageError) as e:
+            capi.set_gemm_config(bad)
+        assert e.value.status == capi.INVALID_REQUEST
