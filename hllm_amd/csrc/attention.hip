@@ -57,13 +57,14 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 2 : 1) attention_mfma_ker
   constexpr int KK = D / 32;  // 32-wide chunks of the QK contraction
   constexpr int DF = D / 16;  // 16-row fragments of O^T
   extern __shared__ float smem[];
-  // Workgroups loop over the work list (its size is written by the pack kernel); a launch
-  // may have fewer workgroups than items.
-  const int count = *a.work_count;
-  for (int wi = blockIdx.x; wi < count; wi += gridDim.x) {
+  // Workgroups loop over (work item, KV head) pairs, KV heads innermost so that the
+  // dispatch follows the list's order (the list's size is written by the pack kernel); a
+  // launch may have fewer workgroups than pairs.
+  const int count = *a.work_count * a.kv_heads;
+  for (int idx = blockIdx.x; idx < count; idx += gridDim.x) {
   [&] {
+  const int wi = idx / a.kv_heads, kvh = idx - wi * a.kv_heads;
   const AttnWork w = a.work[wi];
-  const int kvh = blockIdx.y;
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
   const bool split_keys = nvec <= 16;
@@ -540,7 +541,7 @@ void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
     return true;
   }();
   (void)configured;
-  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_grid, a.kv_heads), kThreads, lds, stream>>>(a); });
+  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a); });
 }
 
 }  // namespace

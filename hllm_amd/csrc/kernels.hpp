@@ -42,17 +42,34 @@ __host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_sp
   const int per = ((keys + splits - 1) / splits + 31) & ~31;
   return per;
 }
-__host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
-                                              int max_splits, int decode_unit) {
+// The work list holds heavy items first: prefill blocks (more than 16 query vectors) and
+// decode-like splits of at least half a decode unit of keys, then the rest. Workgroups are
+// dispatched in list order, so the short items fill in behind the long ones.
+__host__ __device__ inline bool attn_heavy(int per, int vectors, int decode_unit) {
+  return vectors > 16 || 2 * per >= decode_unit;
+}
+// Work items (block x key split) of one query item: heavy and light counts.
+__host__ __device__ inline void attn_item_work_classes(int query_tokens, int first_position, int group,
+                                                       int max_splits, int decode_unit, int& heavy,
+                                                       int& light) {
   const int qb = attn_block_rows(group);
-  int work = 0;
+  heavy = light = 0;
   for (int r0 = 0; r0 < query_tokens; r0 += qb) {
     const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
     const int keys = first_position + r0 + rows;
     const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
-    work += (keys + per - 1) / per;
+    const int splits = (keys + per - 1) / per;
+    if (attn_heavy(per, rows * group, decode_unit))
+      heavy += splits;
+    else
+      light += splits;
   }
-  return work;
+}
+__host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
+                                              int max_splits, int decode_unit) {
+  int heavy, light;
+  attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, heavy, light);
+  return heavy + light;
 }
 
 // Where each packed row of a pass comes from, built on the device from ItemMeta.

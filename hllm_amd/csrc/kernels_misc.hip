@@ -40,29 +40,43 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
                                                      const int32_t* last_token,
                                                      const int32_t* block_table, int table_width,
                                                      int block_tokens, PackOut out) {
-  __shared__ int scratch[12];
+  __shared__ int scratch[20];
   const int i = blockIdx.x;
-  int offset = 0, samples = 0, work = 0;
-  for (int j = threadIdx.x; j < i; j += blockDim.x) {
-    offset += (int)items[j].query_tokens;
-    samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
+  // Prefix sums over the items before this one (rows, samples, heavy and light attention
+  // work items), and the heavy work items of all items.
+  int offset = 0, samples = 0, heavy = 0, light = 0, heavy_all = 0;
+  for (int j = threadIdx.x; j < (out.attn_work ? n_items : i); j += blockDim.x) {
+    int h = 0, l = 0;
     if (out.attn_work)
-      work += attn_item_work((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
-                             out.attn_max_splits, out.attn_decode_unit);
+      attn_item_work_classes((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
+                             out.attn_max_splits, out.attn_decode_unit, h, l);
+    heavy_all += h;
+    if (j < i) {
+      offset += (int)items[j].query_tokens;
+      samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
+      heavy += h;
+      light += l;
+    }
   }
   offset = wave_sum_int(offset);
   samples = wave_sum_int(samples);
-  work = wave_sum_int(work);
+  heavy = wave_sum_int(heavy);
+  light = wave_sum_int(light);
+  heavy_all = wave_sum_int(heavy_all);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     scratch[wave] = offset;
     scratch[4 + wave] = samples;
-    scratch[8 + wave] = work;
+    scratch[8 + wave] = heavy;
+    scratch[12 + wave] = light;
+    scratch[16 + wave] = heavy_all;
   }
   __syncthreads();
   offset = scratch[0] + scratch[1] + scratch[2] + scratch[3];
   samples = scratch[4] + scratch[5] + scratch[6] + scratch[7];
-  work = scratch[8] + scratch[9] + scratch[10] + scratch[11];
+  heavy = scratch[8] + scratch[9] + scratch[10] + scratch[11];
+  light = scratch[12] + scratch[13] + scratch[14] + scratch[15];
+  heavy_all = scratch[16] + scratch[17] + scratch[18] + scratch[19];
   const ItemMeta it = items[i];
   const bool sample = (it.flags & HLLM_ITEM_SAMPLE) != 0;
   if (threadIdx.x == 0) {
@@ -96,13 +110,14 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
       const int keys = first + r0 + rows;
       const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
       const int splits = (keys + per - 1) / per;
+      const bool is_heavy = attn_heavy(per, rows * group, out.attn_decode_unit);
       for (int s = 0; s < splits; ++s) {
-        out.attn_work[work++] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per,
-                                         min(keys, (s + 1) * per)};
+        const int at = is_heavy ? heavy++ : heavy_all + light++;
+        out.attn_work[at] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per, min(keys, (s + 1) * per)};
       }
       for (int r = 0; r < rows; ++r) out.row_splits[offset + r0 + r] = splits;
     }
-    if (i == n_items - 1) *out.attn_count = work;
+    if (i == n_items - 1) *out.attn_count = heavy_all + light;
   }
 }
 
