@@ -52,8 +52,12 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 
 // ---------------------------------------------------------------- MFMA flash attention
 
-template <int D>
-__global__ void __launch_bounds__(kThreads, D <= 128 ? 2 : 1) attention_mfma_kernel(AttentionArgs a) {
+// DEC: every block of the launch is decode-like (at most 16 query vectors). The prefill
+// path is compiled out and each wave holds one tile, not two, which leaves registers for
+// three workgroups per CU (D <= 128): half as many work items again in flight, for about
+// the same bytes in flight.
+template <int D, bool DEC>
+__global__ void __launch_bounds__(kThreads, D <= 128 ? (DEC ? 3 : 2) : 1) attention_mfma_kernel(AttentionArgs a) {
   constexpr int KK = D / 32;  // 32-wide chunks of the QK contraction
   constexpr int DF = D / 16;  // 16-row fragments of O^T
   extern __shared__ float smem[];
@@ -67,7 +71,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 2 : 1) attention_mfma_ker
   const AttnWork w = a.work[wi];
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
-  const bool split_keys = nvec <= 16;
+  const bool split_keys = DEC || nvec <= 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int quad = lane >> 4, col = lane & 15;
   const int vf = split_keys ? 0 : wave;
@@ -197,17 +201,28 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 2 : 1) attention_mfma_ker
     // loads issue as soon as an iteration starts.
     constexpr int stride = 4;
     int t = w.key_begin + 32 * wave;
-    Tile cur, nxt;
-    fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
-    uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
-    for (; t < w.key_end; t += 32 * stride) {
-      const int tn = clamp_tile(t + 32 * stride);
-      fetch(tn, blk_next, nxt);
-      blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
-      // Issue the next tile's loads here, ahead of this tile's MFMAs.
-      __builtin_amdgcn_sched_barrier(0);
-      consume(t, cur);
-      cur = nxt;
+    if constexpr (DEC) {
+      // One tile per wave at a time; the next tile's block is read one iteration early.
+      uint64_t blk = block_of(clamp_tile(t) / bt);
+      for (; t < w.key_end; t += 32 * stride) {
+        Tile cur;
+        fetch(t, blk, cur);
+        blk = block_of(clamp_tile(t + 32 * stride) / bt);
+        consume(t, cur);
+      }
+    } else {
+      Tile cur, nxt;
+      fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
+      uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
+      for (; t < w.key_end; t += 32 * stride) {
+        const int tn = clamp_tile(t + 32 * stride);
+        fetch(tn, blk_next, nxt);
+        blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
+        // Issue the next tile's loads here, ahead of this tile's MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
+        consume(t, cur);
+        cur = nxt;
+      }
     }
   } else {
     // Prefill blocks: every wave needs every tile, so the workgroup stages each 32-key
@@ -530,18 +545,28 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
   }
 }
 
-template <int D>
-void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
+template <int D, bool DEC>
+void launch_mfma_variant(hipStream_t stream, const AttentionArgs& a) {
   // The decode path's merge area and the prefill path's two K/V stages share the memory.
-  const size_t lds = std::max((size_t)(128 + 4 * D * 16) * sizeof(float),
-                              (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
+  const size_t merge = (size_t)(128 + 4 * D * 16) * sizeof(float);
+  const size_t lds = DEC ? merge : std::max(merge, (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
   static const bool configured = [&] {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D, DEC>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return true;
   }();
   (void)configured;
-  observed(kernel_name<D>("attention_mfma_kernel"), [&] { attention_mfma_kernel<D><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a); });
+  observed(kernel_name<D>("attention_mfma_kernel"), [&] {
+    attention_mfma_kernel<D, DEC><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a);
+  });
+}
+
+template <int D>
+void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
+  if (D <= 128 && a.decode_only)
+    launch_mfma_variant<D, true>(stream, a);
+  else
+    launch_mfma_variant<D, false>(stream, a);
 }
 
 }  // namespace

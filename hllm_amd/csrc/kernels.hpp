@@ -161,6 +161,7 @@ struct AttentionArgs {
   const AttnWork* work;        // MFMA path work list, its size (device) and the launch's
   const int32_t* work_count;   // workgroups along x, which loop over the list
   int work_grid;
+  int decode_only;             // every block has at most 16 query vectors
   const int32_t* row_splits;
   const int32_t* row_item;
   const int32_t* row_position;
