@@ -593,6 +593,8 @@ void launch_attention(hipStream_t stream, const AttentionArgs& a) {
     else
       observed("attention_valu_kernel<_Float16>", [&] { attention_valu_kernel<_Float16><<<grid, kThreads, lds, stream>>>(a); });
   }
+  // MFMA-path blocks with a single split write their rows directly.
+  if (mfma_path && !a.any_split) return;
   const unsigned blocks = (unsigned)(a.rows * a.q_heads + 3) / 4;
   const int path = mfma_path ? 1 : 0;
   observed("attention_combine_kernel", [&] {

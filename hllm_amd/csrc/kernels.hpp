@@ -162,6 +162,7 @@ struct AttentionArgs {
   const int32_t* work_count;   // workgroups along x, which loop over the list
   int work_grid;
   int decode_only;             // every block has at most 16 query vectors
+  int any_split;               // some block's keys are split (MFMA path: the combine runs)
   const int32_t* row_splits;
   const int32_t* row_item;
   const int32_t* row_position;
