@@ -20,6 +20,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <string>
 
 namespace hllm_rocm {
 namespace {
@@ -556,7 +557,9 @@ void launch_mfma_variant(hipStream_t stream, const AttentionArgs& a) {
     return true;
   }();
   (void)configured;
-  observed(kernel_name<D>("attention_mfma_kernel"), [&] {
+  // Named as the profiler names the instantiation.
+  static const std::string name = "attention_mfma_kernel<" + std::to_string(D) + (DEC ? ", true>" : ", false>");
+  observed(name.c_str(), [&] {
     attention_mfma_kernel<D, DEC><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a);
   });
 }

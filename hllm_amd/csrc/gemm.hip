@@ -134,9 +134,9 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
   for (int s = 0; s < P; ++s)
     if (base + s < steps) compute(s);
 
-  // Per-wave partial tiles -> one LDS tile. Each K-wave stores its tile in an LDS area of
-  // its own, then every thread sums its elements over the areas in wave order (the order
-  // of a sequential accumulation, so the sum is deterministic) into area 0.
+  // Per-wave partial tiles -> one tile. Each K-wave stores its tile in an LDS area of its
+  // own; each element is then summed over the areas in wave order (the order of a
+  // sequential accumulation, so the sum is deterministic), by the thread that writes it.
   {
     float* mine = lds + (size_t)wk * BM * LDT;
 #pragma unroll
@@ -155,44 +155,59 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
         *reinterpret_cast<floatx4*>(mine + m * LDT + n) = v;
       }
     __syncthreads();
-    if constexpr (WK > 1) {
+  }
+  // Element (m, n .. n + 3) of the tile summed over the K-wave areas in wave order.
+  auto tile_sum = [&](int m, int n) {
+    floatx4 sum = *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
+#pragma unroll
+    for (int t = 1; t < WK; ++t) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(lds + (size_t)t * BM * LDT + m * LDT + n);
+      sum[0] += x[0];
+      sum[1] += x[1];
+      sum[2] += x[2];
+      sum[3] += x[3];
+    }
+    return sum;
+  };
+
+  if (a.ksplit > 1) {
+    // The K split's partial goes straight from the summed areas to memory.
+    if (a.defer_reduce) {
+      // A row-major [M][N] matrix of its own; the consumer of the projection sums the
+      // splits in order.
+      float* ws = a.workspace + (size_t)split * a.M * a.N;
+      const bool vec = (a.N & 3) == 0;
       for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
         const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-        floatx4 sum = *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
+        const int row = tile_m * BM + m, col = tile_n * BN + n;
+        if (row >= M || col >= a.N) continue;
+        const floatx4 sum = tile_sum(m, n);
+        float* dst = ws + (size_t)row * a.N + col;
+        if (vec) {
+          *reinterpret_cast<floatx4*>(dst) = sum;
+        } else {
 #pragma unroll
-        for (int t = 1; t < WK; ++t) {
-          const floatx4 x = *reinterpret_cast<const floatx4*>(lds + (size_t)t * BM * LDT + m * LDT + n);
-          sum[0] += x[0];
-          sum[1] += x[1];
-          sum[2] += x[2];
-          sum[3] += x[3];
+          for (int t = 0; t < 4; ++t)
+            if (col + t < a.N) dst[t] = sum[t];
         }
-        *reinterpret_cast<floatx4*>(lds + m * LDT + n) = sum;
       }
-      __syncthreads();
-    }
-  }
-
-  if (a.ksplit > 1 && a.defer_reduce) {
-    // Partial output of this K split as a row-major [M][N] matrix of its own; the consumer
-    // of the projection sums the splits in order.
-    float* ws = a.workspace + (size_t)split * a.M * a.N;
-    for (int e = threadIdx.x; e < BM * BN; e += NT) {
-      const int m = e / BN, n = e % BN;
-      const int row = tile_m * BM + m, col = tile_n * BN + n;
-      if (row < M && col < a.N) ws[(size_t)row * a.N + col] = lds[m * LDT + n];
+    } else {
+      // A partial tile; gemm_reduce_kernel sums the splits in order and applies the
+      // epilogue after this kernel completes (no device-scope fences needed).
+      float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
+      for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
+        const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
+        *reinterpret_cast<floatx4*>(ws + m * BN + n) = tile_sum(m, n);
+      }
     }
     return;
   }
-  if (a.ksplit > 1) {
-    // Partial tile of this K split; gemm_reduce_kernel sums the splits in order and applies
-    // the epilogue after this kernel completes (no device-scope fences needed).
-    float* ws = a.workspace + ((size_t)tile * a.ksplit + split) * BM * BN;
+  if constexpr (WK > 1) {
     for (int e = threadIdx.x; e < BM * BN / 4; e += NT) {
       const int m = e / (BN / 4), n = (e % (BN / 4)) * 4;
-      *reinterpret_cast<floatx4*>(ws + m * BN + n) = *reinterpret_cast<const floatx4*>(lds + m * LDT + n);
+      *reinterpret_cast<floatx4*>(lds + m * LDT + n) = tile_sum(m, n);
     }
-    return;
+    __syncthreads();
   }
 
   // Epilogue from the LDS tile.
