@@ -20,7 +20,6 @@
 #include "kernels.hpp"
 
 #include <algorithm>
-#include <string>
 
 namespace hllm_rocm {
 namespace {
@@ -53,12 +52,11 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 
 // ---------------------------------------------------------------- MFMA flash attention
 
-// DEC: every block of the launch is decode-like (at most 16 query vectors). The prefill
-// path is compiled out and each wave holds one tile, not two, which leaves registers for
-// three workgroups per CU (D <= 128): half as many work items again in flight, for about
-// the same bytes in flight.
-template <int D, bool DEC>
-__global__ void __launch_bounds__(kThreads, D <= 128 ? (DEC ? 3 : 2) : 1) attention_mfma_kernel(AttentionArgs a) {
+// Three workgroups per CU for D <= 128: decode-like blocks hold one K/V tile per wave at a
+// time (registers for a second one would allow only two), so that more work items are in
+// flight for about the same bytes in flight.
+template <int D>
+__global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_kernel(AttentionArgs a) {
   constexpr int KK = D / 32;  // 32-wide chunks of the QK contraction
   constexpr int DF = D / 16;  // 16-row fragments of O^T
   extern __shared__ float smem[];
@@ -72,7 +70,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? (DEC ? 3 : 2) : 1) attent
   const AttnWork w = a.work[wi];
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
-  const bool split_keys = DEC || nvec <= 16;
+  const bool split_keys = nvec <= 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int quad = lane >> 4, col = lane & 15;
   const int vf = split_keys ? 0 : wave;
@@ -192,38 +190,19 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? (DEC ? 3 : 2) : 1) attent
 
   if (split_keys) {
     // Decode-like blocks: the four waves take interleaved tiles, each loading its own
-    // fragments from HBM straight into registers, one tile ahead.
-    // Loads are issued unconditionally (a tile past the range re-reads the range's last
-    // tile) so that the compiler can count them: the wait before a tile's MFMAs then leaves
-    // the next tile's loads in flight.
+    // fragments from HBM straight into registers, one tile per wave at a time (the other
+    // workgroups on the CU keep the memory busy meanwhile). The next tile's block is read
+    // one iteration early; past the range it re-reads the range's last tile's block.
     const int last_tile = w.key_begin + ((w.key_end - 1 - w.key_begin) & ~31);
     auto clamp_tile = [&](int x) { return x < w.key_end ? x : last_tile; };
-    // The block of the tile after next is read one iteration early, so the next tile's
-    // loads issue as soon as an iteration starts.
     constexpr int stride = 4;
     int t = w.key_begin + 32 * wave;
-    if constexpr (DEC) {
-      // One tile per wave at a time; the next tile's block is read one iteration early.
-      uint64_t blk = block_of(clamp_tile(t) / bt);
-      for (; t < w.key_end; t += 32 * stride) {
-        Tile cur;
-        fetch(t, blk, cur);
-        blk = block_of(clamp_tile(t + 32 * stride) / bt);
-        consume(t, cur);
-      }
-    } else {
-      Tile cur, nxt;
-      fetch(clamp_tile(t), block_of(clamp_tile(t) / bt), cur);
-      uint64_t blk_next = block_of(clamp_tile(t + 32 * stride) / bt);
-      for (; t < w.key_end; t += 32 * stride) {
-        const int tn = clamp_tile(t + 32 * stride);
-        fetch(tn, blk_next, nxt);
-        blk_next = block_of(clamp_tile(t + 64 * stride) / bt);
-        // Issue the next tile's loads here, ahead of this tile's MFMAs.
-        __builtin_amdgcn_sched_barrier(0);
-        consume(t, cur);
-        cur = nxt;
-      }
+    uint64_t blk = block_of(clamp_tile(t) / bt);
+    for (; t < w.key_end; t += 32 * stride) {
+      Tile cur;
+      fetch(t, blk, cur);
+      blk = block_of(clamp_tile(t + 32 * stride) / bt);
+      consume(t, cur);
     }
   } else {
     // Prefill blocks: every wave needs every tile, so the workgroup stages each 32-key
@@ -546,30 +525,19 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
   }
 }
 
-template <int D, bool DEC>
-void launch_mfma_variant(hipStream_t stream, const AttentionArgs& a) {
+template <int D>
+void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
   // The decode path's merge area and the prefill path's two K/V stages share the memory.
-  const size_t merge = (size_t)(128 + 4 * D * 16) * sizeof(float);
-  const size_t lds = DEC ? merge : std::max(merge, (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
+  const size_t lds = std::max((size_t)(128 + 4 * D * 16) * sizeof(float),
+                              (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
   static const bool configured = [&] {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D, DEC>),
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return true;
   }();
   (void)configured;
-  // Named as the profiler names the instantiation.
-  static const std::string name = "attention_mfma_kernel<" + std::to_string(D) + (DEC ? ", true>" : ", false>");
-  observed(name.c_str(), [&] {
-    attention_mfma_kernel<D, DEC><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a);
-  });
-}
-
-template <int D>
-void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
-  if (D <= 128 && a.decode_only)
-    launch_mfma_variant<D, true>(stream, a);
-  else
-    launch_mfma_variant<D, false>(stream, a);
+  observed(kernel_name<D>("attention_mfma_kernel"),
+           [&] { attention_mfma_kernel<D><<<dim3(a.work_grid * a.kv_heads), kThreads, lds, stream>>>(a); });
 }
 
 }  // namespace

@@ -161,7 +161,6 @@ struct AttentionArgs {
   const AttnWork* work;        // MFMA path work list, its size (device) and the launch's
   const int32_t* work_count;   // workgroups along x, which loop over the list
   int work_grid;
-  int decode_only;             // every block has at most 16 query vectors
   int any_split;               // some block's keys are split (MFMA path: the combine runs)
   const int32_t* row_splits;
   const int32_t* row_item;

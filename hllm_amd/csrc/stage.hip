@@ -222,10 +222,10 @@ class Stage {
   // are read on the device); a shape is captured the second time it is seen (the first run
   // sets the kernels' attributes eagerly).
   struct PassShape {
-    uint32_t items, rows, samples, sampler, attention_items, decode_only, any_split;
+    uint32_t items, rows, samples, sampler, attention_items, any_split;
     bool operator<(const PassShape& o) const {
-      return std::tie(items, rows, samples, sampler, attention_items, decode_only, any_split) <
-             std::tie(o.items, o.rows, o.samples, o.sampler, o.attention_items, o.decode_only, o.any_split);
+      return std::tie(items, rows, samples, sampler, attention_items, any_split) <
+             std::tie(o.items, o.rows, o.samples, o.sampler, o.attention_items, o.any_split);
     }
   };
   struct CapturedPass {
@@ -1073,7 +1073,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   }
   int attn_work_count = 0;
   // Every attention block decode-like (at most 16 query vectors): the decode-only kernel.
-  bool attn_decode_only = true, attn_any_split = false;
+  bool attn_any_split = false;
   if (mfma_attention_) {
     const int qb = attn_block_rows((int)(Q_ / K_));
     for (uint32_t i = 0; i < n; ++i) {
@@ -1081,7 +1081,6 @@ void Stage::submit(const hllm_rocm_pass& pass) {
                                       (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit);
       attn_work_count += work;
       attn_any_split |= work > ((int)pass.item[i].query_tokens + qb - 1) / qb;  // more items than blocks
-      attn_decode_only &= pass.item[i].query_tokens * (Q_ / K_) <= 16;
     }
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
@@ -1147,7 +1146,6 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       at.work = attn_work_.as<AttnWork>();
       at.work_count = attn_count_.as<int32_t>();
       at.work_grid = attn_grid;
-      at.decode_only = attn_decode_only ? 1 : 0;
       at.any_split = attn_any_split ? 1 : 0;
       at.row_splits = pack_.row_splits;
       at.q = q_.as<float>();
@@ -1250,7 +1248,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   };
   try {
     const PassShape shape{n, (uint32_t)R, (uint32_t)S, sampler ? 1u : 0u, (uint32_t)attn_grid,
-                          attn_decode_only ? 1u : 0u, attn_any_split ? 1u : 0u};
+                          attn_any_split ? 1u : 0u};
     const bool graphable = graphs_enabled_ && !profiling_ && !pass.logits && !pass.trace_hidden;
     auto found = graphable ? graphs_.find(shape) : graphs_.end();
     if (found != graphs_.end()) {
