@@ -1072,7 +1072,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
     attn_bytes += rows * Q_ * D_ * (4 + 2);
   }
   int attn_work_count = 0;
-  // Every attention block decode-like (at most 16 query vectors): the decode-only kernel.
+  // Some block's keys split in two or more: the split combine runs after the attention.
   bool attn_any_split = false;
   if (mfma_attention_) {
     const int qb = attn_block_rows((int)(Q_ / K_));
