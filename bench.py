@@ -8,7 +8,8 @@ lengths uniform in [64, 256], prefill in chunks of at most 512 tokens per pass m
 the decode rows of every running request. One step = one pass of the stage over one such
 ragged batch; the value is output (sampled) tokens per second over the timed steps.
 
-Also measured: pure decode passes of 64 rows (HBM bytes / step time against 8 TB/s),
+Also measured: pure decode passes of 64 rows (HBM bytes / step time against 8 TB/s and
+against a measured streaming-read ceiling),
 512-token prefill passes (FLOPs / time against 2.5 PFLOP/s dense F16), p50/p99 step
 latency, per-kernel HIP-event roofline of the dominant kernel, and the reference CPU
 worker's arithmetic (oracle/_ref, one thread) timed on this host.
@@ -417,6 +418,9 @@ def main():
     }
     if not args.skip_extras:
         result["decode"] = decode_bench(stage, shape, rng, args.concurrency, args.decode_steps)
+        peak = capi.measure_read_bandwidth(4 << 30)
+        result["decode"]["hbm_read_ceiling_gb_s"] = peak
+        result["decode"]["hbm_frac_of_read_ceiling"] = result["decode"]["hbm_gb_s"] / peak
         log("decode:", json.dumps({k: v for k, v in result["decode"].items() if k != "kernels"}))
         result["prefill"] = [prefill_bench(stage, shape, rng, past, 3) for past in (0, 1536)]
         log("prefill:", json.dumps(result["prefill"]))

@@ -29,7 +29,8 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_stage_wait", "hllm_rocm_stage_last_layout", "hllm_rocm_sequence_blocks",
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
            "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
-           "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config")
+           "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config",
+           "hllm_rocm_measure_read_bandwidth")
 
 
 class StageError(RuntimeError):
@@ -121,6 +122,7 @@ def library() -> C.CDLL:
     L.hllm_rocm_stage_set_graphs.argtypes = [vp, u32]
     L.hllm_rocm_stage_graph_stats.argtypes = [vp, C.POINTER(u64), C.POINTER(u64)]
     L.hllm_rocm_set_gemm_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
+    L.hllm_rocm_measure_read_bandwidth.argtypes = [C.c_int32, u64, C.POINTER(C.c_double)]
     L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
@@ -342,6 +344,13 @@ def sample_logits(logits, options, device: int = 0):
                                              _ptr(tokens, C.c_uint64), _ptr(logprobs, C.c_double),
                                              _ptr(top_ids, C.c_uint64), _ptr(top_lp, C.c_double)))
     return tokens, logprobs, top_ids, top_lp
+
+
+def measure_read_bandwidth(nbytes: int = 4 << 30, device: int = 0) -> float:
+    """Measured HBM read ceiling of the device in GB/s (best of five streaming reads)."""
+    out = C.c_double(0.0)
+    check(library().hllm_rocm_measure_read_bandwidth(device, nbytes, C.byref(out)))
+    return out.value
 
 
 def set_gemm_config(config: int) -> int:

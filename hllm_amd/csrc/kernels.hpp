@@ -116,6 +116,8 @@ __host__ __device__ inline uint64_t kv_value_index(const KvView& kv, int layer, 
          ((uint64_t)(offset >> 5) * kv.head_dim + d) * 32 + (offset & 31);
 }
 
+// Streaming read of `bytes` (a multiple of 16) from p: a measured HBM read ceiling.
+void launch_read_probe(hipStream_t stream, const void* p, size_t bytes, float* out);
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
                  const int32_t* last_token, const int32_t* block_table, int table_width,
                  int block_tokens, PackOut out);

@@ -569,9 +569,31 @@ __global__ void __launch_bounds__(kBlock) relayout_kernel(RelayoutArgs a) {
   if (bad) atomicOr(a.flags, bad);
 }
 
+// ------------------------------------------------------------------ read probe
+
+// Streaming read of n 16-byte words, four loads in flight per thread per iteration; the
+// sum is stored only if it equals a value it never takes, so that the loads stay.
+__global__ void __launch_bounds__(256) read_probe_kernel(const floatx4* p, size_t n, float* out) {
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    const floatx4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+    acc += a + b + c + d;
+  }
+  for (; i < n; i += stride) acc += p[i];
+  if (acc[0] == -1234.5f) out[0] = acc[1];
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
+
+void launch_read_probe(hipStream_t stream, const void* p, size_t bytes, float* out) {
+  observed("read_probe_kernel", [&] {
+    read_probe_kernel<<<512, 256, 0, stream>>>(static_cast<const floatx4*>(p), bytes / 16, out);
+  });
+}
 
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
                  const int32_t* last_token, const int32_t* block_table, int table_width,

@@ -1362,6 +1362,43 @@ void check_sampling(const hllm_rocm_item& it) {
     fail(HLLM_INVALID_REQUEST, "invalid sampling parameters");
 }
 
+// Best of five timed streaming reads of `bytes` (after a warm one), in GB/s.
+double measure_read_bandwidth(int32_t device, uint64_t bytes) {
+  if (bytes < (1u << 20) || bytes % 16 || bytes > (64ull << 30)) fail(HLLM_INVALID_REQUEST, "read probe size");
+  HIP_CHECK(hipSetDevice(device));
+  DeviceMemory buf, out;
+  buf.allocate(bytes, "read probe");
+  out.allocate(sizeof(float), "read probe");
+  hipStream_t s = nullptr;
+  HIP_CHECK(hipStreamCreate(&s));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  double best = 0.0;
+  try {
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    HIP_CHECK(hipMemsetAsync(buf.ptr, 0, bytes, s));
+    launch_read_probe(s, buf.ptr, bytes, out.as<float>());
+    for (int i = 0; i < 5; ++i) {
+      HIP_CHECK(hipEventRecord(e0, s));
+      launch_read_probe(s, buf.ptr, bytes, out.as<float>());
+      HIP_CHECK(hipEventRecord(e1, s));
+      HIP_CHECK(hipEventSynchronize(e1));
+      float ms = 0.f;
+      HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+      best = std::max(best, bytes / (ms * 1e-3) / 1e9);
+    }
+  } catch (...) {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(s);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipStreamDestroy(s);
+  return best;
+}
+
 void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t V, const hllm_rocm_item* options,
                    uint64_t* tokens, double* logprobs, uint64_t* top_ids, double* top_logprobs) {
   if (!logits || !options || !tokens || rows == 0 || V == 0) fail(HLLM_INVALID_REQUEST, "invalid sampling request");
@@ -1598,6 +1635,13 @@ hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled)
 
 hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured, uint64_t* replayed) {
   return guarded([&] { impl(stage).graph_stats(captured, replayed); });
+}
+
+hllm_status hllm_rocm_measure_read_bandwidth(int32_t device, uint64_t bytes, double* gb_s) {
+  return guarded([&] {
+    if (!gb_s) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null output");
+    *gb_s = hllm_rocm::measure_read_bandwidth(device, bytes);
+  });
 }
 
 hllm_status hllm_rocm_set_gemm_config(int32_t config, int32_t* previous) {

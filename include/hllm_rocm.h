@@ -188,6 +188,12 @@ hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled)
 hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured,
                                         uint64_t* replayed);
 
+/* Diagnostics: the HBM read ceiling of `device`, measured as the best of five streaming
+ * reads of `bytes` (at least 1 MiB, a multiple of 16) with a plain read kernel, in GB/s.
+ * For comparing the stage's memory-bound rates with what the device delivers; no
+ * counterpart in the reference. */
+hllm_status hllm_rocm_measure_read_bandwidth(int32_t device, uint64_t bytes, double* gb_s);
+
 /* Tuning and test hook, process-wide: every later projection GEMM uses configuration
  * `config` of the kernel table (0 .. 16) instead of the choice by shape; -1 restores the
  * choice by shape. *previous (may be NULL) receives the value replaced. Results stay within

@@ -76,3 +76,10 @@ def test_gemm_configuration_hook_validates_and_restores():
         with pytest.raises(capi.StageError) as e:
             capi.set_gemm_config(bad)
         assert e.value.status == capi.INVALID_REQUEST
+
+
+def test_read_probe_validates_sizes_before_touching_a_device():
+    for bad in (0, 1000, (1 << 20) + 8, 65 << 30):
+        with pytest.raises(capi.StageError) as e:
+            capi.measure_read_bandwidth(bad)
+        assert e.value.status == capi.INVALID_REQUEST

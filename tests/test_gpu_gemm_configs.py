@@ -92,3 +92,8 @@ def test_forced_configuration_matches_the_oracle(stage, expected, config):
     finally:
         capi.set_gemm_config(previous)
 
+
+def test_read_probe_measures_a_plausible_ceiling():
+    """The read ceiling the benchmark compares decode rates with: between 1 and 8.5 TB/s."""
+    gb_s = capi.measure_read_bandwidth(256 << 20)
+    assert 1000.0 < gb_s < 8500.0, gb_s
