@@ -45,6 +45,11 @@ __device__ inline float wave_sum(float v) {
 __device__ inline float rescale(float m, float reference) {
   return m == -INFINITY ? 0.0f : expf(m - reference);
 }
+// The MFMA kernel keeps scores in base 2 (log2 e folded into the query scale): 2^x is one
+// v_exp_f32, which also maps -inf to 0.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int split) {
   return a.partial + (((size_t)row * a.q_heads + qh) * a.max_splits + split) * (a.head_dim + 2);
@@ -91,7 +96,8 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   };
   const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
 
-  // Q^T as the B operand (1/sqrt(D) folded in): lane holds Q[v][32 kk + 8 quad + j].
+  // Q^T as the B operand (1/sqrt(D) and log2 e folded in): lane holds Q[v][32 kk + 8 quad + j].
+  const float qscale = a.scale * kLog2e;
   half8 qf[KK];
   {
     const float* qrow = a.q + ((size_t)(w.row0 + (v_ok ? vr : 0)) * a.q_heads + kvh * G + vg) * D;
@@ -101,8 +107,8 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
       const floatx4 x1 = *reinterpret_cast<const floatx4*>(qrow + 32 * kk + 8 * quad + 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        qf[kk][j] = v_ok ? to_half(x0[j] * a.scale) : (_Float16)0.0f;
-        qf[kk][4 + j] = v_ok ? to_half(x1[j] * a.scale) : (_Float16)0.0f;
+        qf[kk][j] = v_ok ? to_half(x0[j] * qscale) : (_Float16)0.0f;
+        qf[kk][4 + j] = v_ok ? to_half(x1[j] * qscale) : (_Float16)0.0f;
       }
     }
   }
@@ -142,12 +148,24 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     s0 = mfma(f.k0[kk], qf[kk], s0);
     s1 = mfma(f.k1[kk], qf[kk], s1);
   }
+  // Scores (base 2) of the tile's positions, -inf past the key range or the vector's own
+  // position. A tile wholly before the block's first position and inside the range needs
+  // no mask (the usual case). Vectors past the block's end are not masked: their results
+  // are never written.
   float sc[8];
+  if (t + 32 <= w.key_end && t + 31 <= w.position0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
-    sc[i] = (v_ok && p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
-    sc[4 + i] = (v_ok && p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = s0[i];
+      sc[4 + i] = s1[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
+      sc[i] = (p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
+      sc[4 + i] = (p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+    }
   }
   float tmax = sc[0];
 #pragma unroll
@@ -156,12 +174,12 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
   const float m_new = fmaxf(m, tmax);
   const float base = m_new == -INFINITY ? 0.0f : m_new;
-  const float alpha = rescale(m, base);
+  const float alpha = exp2_fast(m - base);
   half8 pf;
   float psum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float p = sc[i] == -INFINITY ? 0.0f : expf(sc[i] - base);
+    const float p = exp2_fast(sc[i] - base);
     psum += p;
     pf[i] = to_half(p);
   }
@@ -205,64 +223,87 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
       consume(t, cur);
     }
   } else {
-    // Prefill blocks: every wave needs every tile, so the workgroup stages each 32-key
-    // tile once in LDS (double-buffered; the next tile's global loads are in flight while
-    // this one is used). Keys are rows of D + 8 halves (the pad spreads the permuted rows
-    // of a fragment over the LDS banks), values the tile's [D][32] sub-tile as stored.
-    constexpr int KROW = D + 8;
-    constexpr int STAGE = 32 * KROW + D * 32;  // halves per stage
-    constexpr int PIECES = D / 32;             // 16-byte pieces per thread per tile
-    _Float16* stage = reinterpret_cast<_Float16*>(smem);
-    half8 staged[PIECES];
-    auto load_tile = [&](int t) {
-      const uint64_t blk = block_of(t / bt);
+    // Prefill blocks: every wave needs every tile, so the workgroup copies each 32-key K/V
+    // tile once into LDS, straight from the cache (global_load_lds), NSTAGE tiles deep: the
+    // copies of tiles i + 1 and i + 2 are in flight while tile i is used. Keys are the tile's
+    // 32 x D rows and values its [D][32] sub-tile, both with their 16-byte chunks permuted
+    // per row (chunk c of key row r at c ^ key_swizzle(r), of value row d at
+    // c ^ ((d >> 2) & 3)) so that the fragment reads below hit distinct LDS banks.
+    constexpr int KB = 32 * D * 2;              // key bytes per tile
+    constexpr int SB = KB + D * 32 * 2;         // key and value bytes per tile
+    constexpr int NSTAGE = 3;
+    constexpr int CP = SB / (kThreads * 16);    // 16-byte copies per lane per tile
+    static_assert(SB % (kThreads * 16) == 0 && KB % (kThreads * 16) == 0, "attention tile copies");
+    const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)smem);
+    auto key_swizzle = [](int r) {
+      return D >= 128 ? (r & 3) | (((r >> 3) & 3) << 2) : ((r >> 1) & 1) | (((r >> 3) & 3) << 1);
+    };
+    const int tiles = (w.key_end - w.key_begin + 31) / 32;
+    // Block-table entries of the range, one per lane, 64 blocks at a time: a table read
+    // inside the pipelined loop would be a vector load (the copies clobber memory as far as
+    // the compiler knows), and waiting for it would drain the copies in flight.
+    const int last_block = (w.key_end - 1) / bt;
+    int held_base = 0, held = 0;
+    // This wave's copies of tile i into stage i % NSTAGE: wave-sized 1 KiB pieces of the
+    // stage, interleaved over the waves, the first KB / 1024 of them keys.
+    auto issue = [&](int i) {
+      const int t = w.key_begin + 32 * i;
+      const uint64_t blk = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(held, t / bt - held_base);
       const int off = t % bt;
       const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
       const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
+      const uint32_t stage = lds_base + (uint32_t)(i % NSTAGE) * SB;
 #pragma unroll
-      for (int q = 0; q < PIECES; ++q) {
-        const int e = threadIdx.x + q * kThreads;  // < 8 D: 4 D key pieces, then 4 D value pieces
-        staged[q] = e < 4 * D ? *reinterpret_cast<const half8*>(kb + (size_t)e * 8)
-                              : *reinterpret_cast<const half8*>(vb + (size_t)(e - 4 * D) * 8);
-      }
-    };
-    auto store_tile = [&](int buffer) {
-      _Float16* dst = stage + buffer * STAGE;
-#pragma unroll
-      for (int q = 0; q < PIECES; ++q) {
-        const int e = threadIdx.x + q * kThreads;
-        if (e < 4 * D) {
-          const int row = e / (D / 8), c8 = e - row * (D / 8);
-          *reinterpret_cast<half8*>(dst + row * KROW + c8 * 8) = staged[q];
+      for (int q = 0; q < CP; ++q) {
+        const int piece = q * (kThreads / 64) + wave;
+        const int p = piece * 1024 + lane * 16;  // this lane's byte in the stage
+        if (q * (kThreads / 64) * 1024 < KB) {
+          const int r = p / (2 * D), c = (p % (2 * D)) / 16;
+          lds_copy16(kb, (uint32_t)(r * 2 * D + ((c ^ key_swizzle(r)) * 16)), stage + piece * 1024);
         } else {
-          *reinterpret_cast<half8*>(dst + 32 * KROW + (e - 4 * D) * 8) = staged[q];
+          const int d = (p - KB) / 64, c = ((p - KB) % 64) / 16;
+          lds_copy16(vb, (uint32_t)(d * 64 + ((c ^ ((d >> 2) & 3)) * 16)), stage + piece * 1024);
         }
       }
     };
     auto read_tile = [&](int buffer, Tile& f) {
-      const _Float16* ks = stage + buffer * STAGE;
-      const _Float16* vs = ks + 32 * KROW;
+      const char* ks = reinterpret_cast<const char*>(smem) + buffer * SB;
+      const char* vs = ks + KB;
       const int r0 = 8 * (col >> 2) + (col & 3);  // the permuted key rows of fetch()
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        f.k0[kk] = *reinterpret_cast<const half8*>(ks + r0 * KROW + 32 * kk + 8 * quad);
-        f.k1[kk] = *reinterpret_cast<const half8*>(ks + (r0 + 4) * KROW + 32 * kk + 8 * quad);
+        const int c = 4 * kk + quad;
+        f.k0[kk] = *reinterpret_cast<const half8*>(ks + r0 * 2 * D + ((c ^ key_swizzle(r0)) * 16));
+        f.k1[kk] = *reinterpret_cast<const half8*>(ks + (r0 + 4) * 2 * D + ((c ^ key_swizzle(r0 + 4)) * 16));
       }
 #pragma unroll
-      for (int df = 0; df < DF; ++df) f.v[df] = *reinterpret_cast<const half8*>(vs + (16 * df + col) * 32 + 8 * quad);
+      for (int df = 0; df < DF; ++df) {
+        const int d = 16 * df + col;
+        f.v[df] = *reinterpret_cast<const half8*>(vs + d * 64 + ((quad ^ ((d >> 2) & 3)) * 16));
+      }
     };
-    const int tiles = (w.key_end - w.key_begin + 31) / 32;
-    load_tile(w.key_begin);
-    store_tile(0);
-    __syncthreads();
-    for (int i = 0; i < tiles; ++i) {
-      const int t = w.key_begin + 32 * i;
-      if (i + 1 < tiles) load_tile(t + 32);  // workgroup-uniform
-      Tile f;
-      read_tile(i & 1, f);
-      consume(t, f);
-      if (i + 1 < tiles) store_tile((i + 1) & 1);
-      __syncthreads();
+    for (int i0 = 0; i0 < tiles;) {
+      // Tiles [i0, i1) lie in the 64 blocks held from held_base; the pipeline restarts
+      // after each such group (ranges of more than 64 blocks only).
+      held_base = (w.key_begin + 32 * i0) / bt;
+      held = table[min(held_base + lane, last_block)];
+      const int i1 = min(tiles, ((held_base + 64) * bt - w.key_begin) / 32);
+      issue(i0);
+      if (i0 + 1 < i1) issue(i0 + 1);
+      for (int i = i0; i < i1; ++i) {
+        // Tile i has landed once this wave's later copies (tile i + 1's) are all that is
+        // outstanding and every wave has got here; that also means every wave is done
+        // with tile i - 1, whose stage tile i + 2 overwrites.
+        if (i + 1 < i1)
+          stage_barrier<CP, 0>();
+        else
+          stage_barrier<0, 0>();
+        if (i + 2 < i1) issue(i + 2);  // workgroup-uniform
+        Tile f;
+        read_tile(i % NSTAGE, f);
+        consume(w.key_begin + 32 * i, f);
+      }
+      i0 = i1;
     }
   }
 
@@ -289,7 +330,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     l_fin = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
-      weights[ww] = rescale(sm_m[ww * 16 + col], mm == -INFINITY ? 0.0f : mm);
+      weights[ww] = exp2_fast(sm_m[ww * 16 + col] - (mm == -INFINITY ? 0.0f : mm));
       l_fin += sm_l[ww * 16 + col] * weights[ww];
     }
     m_fin = mm;
@@ -322,7 +363,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[16 * df + 4 * quad + i] = o[df][i];
     if (quad == 0) {
-      out[D] = m_fin;
+      out[D] = m_fin * kLn2;  // the combine kernel takes natural-log maxima
       out[D + 1] = l_fin;
     }
   }
@@ -527,9 +568,9 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
 
 template <int D>
 void launch_mfma(hipStream_t stream, const AttentionArgs& a) {
-  // The decode path's merge area and the prefill path's two K/V stages share the memory.
+  // The decode path's merge area and the prefill path's three K/V stages share the memory.
   const size_t lds = std::max((size_t)(128 + 4 * D * 16) * sizeof(float),
-                              (size_t)2 * (32 * (D + 8) + D * 32) * sizeof(_Float16));
+                              (size_t)3 * (32 * D + D * 32) * sizeof(_Float16));
   static const bool configured = [&] {
     HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_mfma_kernel<D>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));

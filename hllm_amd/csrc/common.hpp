@@ -108,4 +108,33 @@ __device__ inline float from_half_bits(uint16_t b) {
 //   3: split activations x split weights (F32 execution over F32-resident weights)
 enum Precision : int { kF16 = 1, kSplitA = 2, kSplitAB = 3 };
 
+// ------------------------------------------------------------ direct copies to LDS
+
+// One 16-byte copy per lane from sbase + voffset to LDS byte m0 + 16 * lane; sbase and
+// the LDS offset are uniform over the wave.
+__device__ inline void lds_copy16(const void* sbase, uint32_t voffset, uint32_t lds_byte_offset) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voffset), "s"(sbase),
+               "s"(lds_byte_offset)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// s_waitcnt with the given vector-memory and LDS counts (expcnt left open). Issued through
+// the builtin so that the compiler knows which of its own LDS reads have completed.
+template <int vm, int lgkm>
+__device__ inline void wait_counts() {
+  static_assert(vm >= 0 && vm < 64 && lgkm >= 0 && lgkm < 16, "s_waitcnt field range");
+  __builtin_amdgcn_s_waitcnt((vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (lgkm << 8));
+}
+
+// Wait until at most `in_flight` of this wave's copies are outstanding and all but its
+// last `reads` LDS reads have returned, then meet the other waves.
+template <int in_flight, int reads>
+__device__ inline void stage_barrier() {
+  wait_counts<in_flight, reads>();
+  asm volatile("s_barrier" ::: "memory");
+}
+
 }  // namespace hllm_rocm

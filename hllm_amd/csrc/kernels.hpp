@@ -31,45 +31,46 @@ struct AttnWork {
 // at least one row.
 __host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ? 1 : 64 / group; }
 
+// Keys per split of prefill blocks (more than 16 query vectors).
+constexpr int kAttnPrefillUnit = 1024;
+
 // Splits of a block's `keys` key positions, 32-key aligned and non-empty: every
-// `decode_unit` keys (a multiple of 32; 256 by default) for decode-like blocks (at most 16 query vectors: the workgroup's four waves share the
-// keys, and short splits balance rows of very different context lengths), every 1024 keys
-// for prefill blocks (fewer partial results to combine).
+// `decode_unit` keys (a multiple of 32; 256 by default) for decode-like blocks (at most 16
+// query vectors: the workgroup's four waves share the keys, and short splits balance rows
+// of very different context lengths), every kAttnPrefillUnit keys for prefill blocks.
 __host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits, int decode_unit) {
-  const int unit = vectors <= 16 ? decode_unit : 1024;
+  const int unit = vectors <= 16 ? decode_unit : kAttnPrefillUnit;
   int splits = (keys + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = ((keys + splits - 1) / splits + 31) & ~31;
   return per;
 }
-// The work list holds heavy items first: prefill blocks (more than 16 query vectors) and
-// decode-like splits of at least half a decode unit of keys, then the rest. Workgroups are
-// dispatched in list order, so the short items fill in behind the long ones.
-__host__ __device__ inline bool attn_heavy(int per, int vectors, int decode_unit) {
-  return vectors > 16 || 2 * per >= decode_unit;
+// The work list is ordered by dispatch class: prefill blocks (more than 16 query vectors,
+// each an MFMA-bound chain over its key tiles; within an item the blocks with the most keys
+// first), then decode-like splits of at least half a decode unit of keys, then the rest.
+// Workgroups are dispatched in list order, so the short items fill in behind the long ones.
+constexpr int kAttnClasses = 3;
+__host__ __device__ inline int attn_work_class(int per, int vectors, int decode_unit) {
+  return vectors > 16 ? 0 : 2 * per >= decode_unit ? 1 : 2;
 }
-// Work items (block x key split) of one query item: heavy and light counts.
+// Work items (block x key split) of one query item, per dispatch class.
 __host__ __device__ inline void attn_item_work_classes(int query_tokens, int first_position, int group,
-                                                       int max_splits, int decode_unit, int& heavy,
-                                                       int& light) {
+                                                       int max_splits, int decode_unit,
+                                                       int (&count)[kAttnClasses]) {
   const int qb = attn_block_rows(group);
-  heavy = light = 0;
+  for (int c = 0; c < kAttnClasses; ++c) count[c] = 0;
   for (int r0 = 0; r0 < query_tokens; r0 += qb) {
     const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
     const int keys = first_position + r0 + rows;
     const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
-    const int splits = (keys + per - 1) / per;
-    if (attn_heavy(per, rows * group, decode_unit))
-      heavy += splits;
-    else
-      light += splits;
+    count[attn_work_class(per, rows * group, decode_unit)] += (keys + per - 1) / per;
   }
 }
 __host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
                                               int max_splits, int decode_unit) {
-  int heavy, light;
-  attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, heavy, light);
-  return heavy + light;
+  int count[kAttnClasses];
+  attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, count);
+  return count[0] + count[1] + count[2];
 }
 
 // Where each packed row of a pass comes from, built on the device from ItemMeta.

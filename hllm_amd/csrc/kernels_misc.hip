@@ -40,43 +40,38 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
                                                      const int32_t* last_token,
                                                      const int32_t* block_table, int table_width,
                                                      int block_tokens, PackOut out) {
-  __shared__ int scratch[20];
+  __shared__ int scratch[4 * (2 + 2 * kAttnClasses)];
   const int i = blockIdx.x;
-  // Prefix sums over the items before this one (rows, samples, heavy and light attention
-  // work items), and the heavy work items of all items.
-  int offset = 0, samples = 0, heavy = 0, light = 0, heavy_all = 0;
+  // Prefix sums over the items before this one (rows, samples, attention work items per
+  // dispatch class), and the attention work items of all items per class.
+  int offset = 0, samples = 0, before[kAttnClasses] = {0, 0, 0}, all[kAttnClasses] = {0, 0, 0};
   for (int j = threadIdx.x; j < (out.attn_work ? n_items : i); j += blockDim.x) {
-    int h = 0, l = 0;
+    int c[kAttnClasses] = {0, 0, 0};
     if (out.attn_work)
       attn_item_work_classes((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
-                             out.attn_max_splits, out.attn_decode_unit, h, l);
-    heavy_all += h;
+                             out.attn_max_splits, out.attn_decode_unit, c);
+    for (int k = 0; k < kAttnClasses; ++k) all[k] += c[k];
     if (j < i) {
       offset += (int)items[j].query_tokens;
       samples += (items[j].flags & HLLM_ITEM_SAMPLE) ? 1 : 0;
-      heavy += h;
-      light += l;
+      for (int k = 0; k < kAttnClasses; ++k) before[k] += c[k];
     }
   }
-  offset = wave_sum_int(offset);
-  samples = wave_sum_int(samples);
-  heavy = wave_sum_int(heavy);
-  light = wave_sum_int(light);
-  heavy_all = wave_sum_int(heavy_all);
+  int sums[2 + 2 * kAttnClasses] = {offset, samples, before[0], before[1], before[2], all[0], all[1], all[2]};
   const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    scratch[wave] = offset;
-    scratch[4 + wave] = samples;
-    scratch[8 + wave] = heavy;
-    scratch[12 + wave] = light;
-    scratch[16 + wave] = heavy_all;
+  for (int k = 0; k < 2 + 2 * kAttnClasses; ++k) {
+    sums[k] = wave_sum_int(sums[k]);
+    if ((threadIdx.x & 63) == 0) scratch[4 * k + wave] = sums[k];
   }
   __syncthreads();
-  offset = scratch[0] + scratch[1] + scratch[2] + scratch[3];
-  samples = scratch[4] + scratch[5] + scratch[6] + scratch[7];
-  heavy = scratch[8] + scratch[9] + scratch[10] + scratch[11];
-  light = scratch[12] + scratch[13] + scratch[14] + scratch[15];
-  heavy_all = scratch[16] + scratch[17] + scratch[18] + scratch[19];
+  for (int k = 0; k < 2 + 2 * kAttnClasses; ++k)
+    sums[k] = scratch[4 * k] + scratch[4 * k + 1] + scratch[4 * k + 2] + scratch[4 * k + 3];
+  offset = sums[0];
+  samples = sums[1];
+  // Next list slot of each class: the class's base (the classes before it, all items) plus
+  // this class's work of the items before this one.
+  int next[kAttnClasses] = {sums[2], sums[5] + sums[3], sums[5] + sums[6] + sums[4]};
+  const int total = sums[5] + sums[6] + sums[7];
   const ItemMeta it = items[i];
   const bool sample = (it.flags & HLLM_ITEM_SAMPLE) != 0;
   if (threadIdx.x == 0) {
@@ -101,23 +96,23 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     out.row_token[r] = (it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) ? last_token[it.sequence]
                                                                  : host_tokens[r];
   }
-  // Attention blocks of this item: query rows [r0, r0 + rows) against keys [0, first + r0 + rows).
+  // Attention blocks of this item: query rows [r0, r0 + rows) against keys [0, first + r0 + rows),
+  // the last block (most keys) first.
   if (out.attn_work && threadIdx.x == 0) {
     const int group = out.attn_group, qb = attn_block_rows(group);
     const int q = (int)it.query_tokens, first = (int)it.first_position;
-    for (int r0 = 0; r0 < q; r0 += qb) {
+    for (int r0 = (q - 1) / qb * qb; r0 >= 0; r0 -= qb) {
       const int rows = min(qb, q - r0);
       const int keys = first + r0 + rows;
       const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
       const int splits = (keys + per - 1) / per;
-      const bool is_heavy = attn_heavy(per, rows * group, out.attn_decode_unit);
-      for (int s = 0; s < splits; ++s) {
-        const int at = is_heavy ? heavy++ : heavy_all + light++;
-        out.attn_work[at] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per, min(keys, (s + 1) * per)};
-      }
+      const int cls = attn_work_class(per, rows * group, out.attn_decode_unit);
+      for (int s = 0; s < splits; ++s)
+        out.attn_work[next[cls]++] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per,
+                                              min(keys, (s + 1) * per)};
       for (int r = 0; r < rows; ++r) out.row_splits[offset + r0 + r] = splits;
     }
-    if (i == n_items - 1) *out.attn_count = heavy_all + light;
+    if (i == n_items - 1) *out.attn_count = total;
   }
 }
 
