@@ -70,7 +70,13 @@ ITEM_DTYPE = np.dtype({"names": [f for f, _ in capi.Item._fields_],
 
 class Engine:
     """Continuous batching over one stage: every running request contributes one decode row
-    (its input token fed from the device), and prefilling requests share a chunk budget."""
+    (its input token fed from the device), and prefilling requests share a chunk budget.
+
+    Steps are pipelined on the host: a step's effect on the requests (positions, finished
+    outputs) does not depend on the sampled token values, so the next pass is planned and its
+    inputs built while the current one runs, and submitted as soon as it completes
+    (hllm_rocm_stage_submit / hllm_rocm_stage_wait). Sequences of finished requests are
+    released only after their last pass has completed."""
 
     def __init__(self, stage, concurrency, chunk, stream):
         self.stage, self.concurrency, self.chunk, self.stream = stage, concurrency, chunk, stream
@@ -78,13 +84,17 @@ class Engine:
         self.active = []
         self.clock = 0
         self.next_req = next(stream)
-        self.items = np.zeros(concurrency + chunk, ITEM_DTYPE)
-        self.items["top_p"] = 1.0
-        self.ids = np.zeros(concurrency + chunk + 8, np.uint64)
-        self.tokens_out = np.zeros(concurrency + chunk, np.uint64)
-        self.p = capi.Pass()
+        self.buffers = []
+        for _ in range(2):  # the pass in flight keeps its output buffer until it completes
+            items = np.zeros(concurrency + chunk, ITEM_DTYPE)
+            items["top_p"] = 1.0
+            self.buffers.append((items, np.zeros(concurrency + chunk + 8, np.uint64),
+                                 np.zeros(concurrency + chunk, np.uint64), capi.Pass()))
+        self.flip = 0
+        self.current = None  # the submitted pass: (sampled, rows, decode rows, finished)
 
-    def step(self):
+    def _plan(self):
+        """Admits arrivals and builds the next pass; None for an idle step."""
         while self.next_req.arrival <= self.clock:
             self.waiting.append(self.next_req)
             self.next_req = next(self.stream)
@@ -92,14 +102,16 @@ class Engine:
             r = self.waiting.popleft()
             r.seq = self.stage.allocate(len(r.prompt) + r.out_len)
             self.active.append(r)
+        items, ids, tokens_out, p = self.buffers[self.flip]
+        self.flip ^= 1
         n = rows = 0
         decode, prefill = [], []
         for r in self.active:
             if r.fed == len(r.prompt):
-                it = self.items[n]
+                it = items[n]
                 it["sequence"], it["query_tokens"], it["first_position"] = r.seq, 1, r.length
                 it["flags"] = capi.ITEM_SAMPLE | capi.ITEM_TOKEN_FROM_DEVICE
-                self.ids[rows] = 0
+                ids[rows] = 0
                 n, rows = n + 1, rows + 1
                 decode.append(r)
         budget = self.chunk
@@ -108,21 +120,28 @@ class Engine:
                 break
             if r.fed < len(r.prompt):
                 take = min(budget, len(r.prompt) - r.fed)
-                it = self.items[n]
+                it = items[n]
                 it["sequence"], it["query_tokens"], it["first_position"] = r.seq, take, r.length
                 it["flags"] = capi.ITEM_SAMPLE if r.fed + take == len(r.prompt) else 0
-                self.ids[rows:rows + take] = r.prompt[r.fed:r.fed + take]
+                ids[rows:rows + take] = r.prompt[r.fed:r.fed + take]
                 n, rows, budget = n + 1, rows + take, budget - take
                 prefill.append((r, take))
-        if n == 0:  # nothing has arrived yet: an idle step launches nothing
-            self.clock += 1
-            return 0, 0, 0
-        p = self.p
+        if n == 0:
+            return None
         p.items = n
-        p.item = self.items.ctypes.data_as(C.POINTER(capi.Item))
-        p.token_ids = self.ids.ctypes.data_as(C.POINTER(C.c_uint64))
-        p.tokens = self.tokens_out.ctypes.data_as(C.POINTER(C.c_uint64))
-        capi.check(self.stage.lib.hllm_rocm_stage_execute(self.stage.handle, C.byref(p)))
+        p.item = items.ctypes.data_as(C.POINTER(capi.Item))
+        p.token_ids = ids.ctypes.data_as(C.POINTER(C.c_uint64))
+        p.tokens = tokens_out.ctypes.data_as(C.POINTER(C.c_uint64))
+        return p, rows, decode, prefill
+
+    def _launch(self, plan):
+        """Submits a planned pass (nothing for an idle step) and applies its effect on the
+        requests; finished requests leave the running set now."""
+        self.clock += 1
+        if plan is None:  # nothing has arrived yet: an idle step launches nothing
+            return (0, 0, 0, [], False)
+        p, rows, decode, prefill = plan
+        capi.check(self.stage.lib.hllm_rocm_stage_submit(self.stage.handle, C.byref(p)))
         sampled = len(decode)
         finished = []
         for r in decode:
@@ -137,12 +156,30 @@ class Engine:
                 r.generated = 1
                 sampled += 1
         for r in finished:
-            self.stage.release(r.seq)
             self.active.remove(r)
-        self.clock += 1
-        return sampled, rows, len(decode)
+        return (sampled, rows, len(decode), finished, True)
+
+    def step(self, last=False):
+        """Completes one step; unless `last`, the next one is planned while it runs and
+        submitted when it completes. Returns (sampled tokens, rows, decode rows)."""
+        if self.current is None:
+            self.current = self._launch(self._plan())
+        sampled, rows, decode, finished, submitted = self.current
+        plan = None if last else self._plan()
+        if submitted:
+            capi.check(self.stage.lib.hllm_rocm_stage_wait(self.stage.handle))
+        for r in finished:
+            self.stage.release(r.seq)
+        self.current = None if last else self._launch(plan)
+        return sampled, rows, decode
+
+    def drain(self):
+        """Completes the pass in flight without starting another."""
+        if self.current is not None:
+            self.step(last=True)
 
     def release_all(self):
+        self.drain()
         for r in self.active:
             self.stage.release(r.seq)
         self.active = []
@@ -337,6 +374,7 @@ def main():
         if i == max(0, args.warmup - 20):
             stage.profile("*")
         engine.step()
+    engine.drain()
     records = stage.profile_records()
     fam = {r: stage.profile_read(r) for r in records if "/" not in r and not r.startswith("k:")}
     kern = {r[2:]: stage.profile_read(r) for r in records if r.startswith("k:")}
@@ -350,11 +388,12 @@ def main():
         f"(launched by {owners})")
 
     stage.profile(None)
+    # The timed region starts with no pass in flight and ends when its K-th pass completes.
     step_ms, tokens, rows_total, decode_rows = [], 0, 0, 0
     t_start = time.perf_counter()
     for i in range(args.steps):
         t0 = time.perf_counter()
-        s, r, d = engine.step()
+        s, r, d = engine.step(last=i == args.steps - 1)
         step_ms.append(1e3 * (time.perf_counter() - t0))
         tokens += s
         rows_total += r
@@ -366,7 +405,7 @@ def main():
     stage.profile("k:" + dominant)
     t_prof = time.perf_counter()
     for i in range(args.steps):
-        engine.step()
+        engine.step(last=i == args.steps - 1)
     prof_elapsed = time.perf_counter() - t_prof
     dom_ms, dom_n, dom_bytes, dom_flops = stage.profile_read("k:" + dominant)
     stage.profile(None)

@@ -1,0 +1,70 @@
+"""The benchmark's continuous-batching engine against a stand-in stage (no GPU): with the next
+pass planned while the current one runs, every pass still starts each sequence at its current
+length, at most one pass is in flight, no sequence is released or reused while a pass that
+reads it is in flight, and a drained timed region holds exactly the passes it counts."""
+import numpy as np
+
+import bench
+from hllm_amd import capi
+
+
+class _Lib:
+    def __init__(self, stage):
+        self.stage = stage
+
+    def hllm_rocm_stage_submit(self, handle, pass_ref):
+        st = self.stage
+        assert st.in_flight is None, "a pass is already in flight"
+        p = pass_ref._obj
+        used = set()
+        for i in range(p.items):
+            it = p.item[i]
+            assert st.live.get(it.sequence), "pass over a released sequence"
+            assert it.first_position == st.length[it.sequence]
+            assert it.query_tokens >= 1 and it.sequence not in used
+            st.length[it.sequence] += it.query_tokens
+            used.add(it.sequence)
+        st.in_flight = used
+        st.passes += 1
+        return 0
+
+    def hllm_rocm_stage_wait(self, handle):
+        assert self.stage.in_flight is not None, "no pass in flight"
+        self.stage.in_flight = None
+        return 0
+
+
+class _Stage:
+    handle = None
+
+    def __init__(self):
+        self.count, self.length, self.live, self.in_flight, self.passes = 0, {}, {}, None, 0
+        self.lib = _Lib(self)
+
+    def allocate(self, tokens):
+        self.count += 1
+        self.length[self.count], self.live[self.count] = 0, True
+        return self.count
+
+    def release(self, seq):
+        assert self.in_flight is None or seq not in self.in_flight, "released while in flight"
+        assert self.live[seq]
+        self.live[seq] = False
+
+
+def test_pipelined_engine_keeps_sequence_state(monkeypatch):
+    monkeypatch.setattr(capi, "check", lambda status: None)
+    stage = _Stage()
+    engine = bench.Engine(stage, 16, 64, bench.request_stream(np.random.default_rng(3), 1000, 1.0))
+    for _ in range(150):
+        engine.step()
+    engine.drain()
+    assert stage.in_flight is None
+    before = stage.passes
+    tokens = 0
+    for i in range(200):
+        tokens += engine.step(last=i == 199)[0]
+    assert stage.in_flight is None and stage.passes - before == 200
+    assert tokens > 0
+    engine.release_all()
+    assert not any(stage.live.values())
