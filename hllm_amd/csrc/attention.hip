@@ -6,9 +6,9 @@
 // (v_mfma_f32_16x16x32_f16 with a cached key fragment as the A operand, loaded straight
 // from the paged cache), so that each lane holds four positions of one query vector; the
 // probabilities of 32 positions then form the B operand of O^T = V^T P directly in
-// registers: both operands list the positions in the same k-slot order (key rows are loaded
-// permuted so a lane's scores are 8 consecutive positions, and the values are stored
-// transposed per block, so each V^T row segment is one 16-byte load). Online softmax runs in
+// registers: both operands list the positions in the same k-slot order (keys are stored in
+// operand order with their rows permuted so a lane's scores are 8 consecutive positions, and
+// the values are stored transposed per block, so each V^T row segment is one 16-byte load). Online softmax runs in
 // F32 per query vector. Blocks of at most 16 vectors (decode rows) let the four waves
 // interleave 32-key tiles and merge through LDS; larger blocks give each wave 16 vectors.
 //
@@ -126,14 +126,14 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     const int off = t % bt;
     const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
     const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
-    // Key rows are permuted so that score fragment 0 row 4q+i is position 8q+i and fragment
-    // 1 row 4q+i is position 8q+4+i: lane (q, v) then holds the scores of the 8 consecutive
-    // positions 8q..8q+7, which is also the order of its 16-byte V^T load.
-    const int r0 = 8 * (col >> 2) + (col & 3);
+    // The tile's keys are stored as the operands themselves (kv_key_index): score
+    // fragment 0 row 4q+i is position 8q+i and fragment 1 row 4q+i is position 8q+4+i, so
+    // lane (q, v) holds the scores of the 8 consecutive positions 8q..8q+7, which is also
+    // the order of its 16-byte V^T load. Each operand is one contiguous 1 KiB load.
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      f.k0[kk] = *reinterpret_cast<const half8*>(kb + (size_t)r0 * D + 32 * kk + 8 * quad);
-      f.k1[kk] = *reinterpret_cast<const half8*>(kb + (size_t)(r0 + 4) * D + 32 * kk + 8 * quad);
+      f.k0[kk] = *reinterpret_cast<const half8*>(kb + (size_t)((2 * kk) * 64 + lane) * 8);
+      f.k1[kk] = *reinterpret_cast<const half8*>(kb + (size_t)((2 * kk + 1) * 64 + lane) * 8);
     }
 #pragma unroll
     for (int df = 0; df < DF; ++df) {
@@ -225,9 +225,9 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   } else {
     // Prefill blocks: every wave needs every tile, so the workgroup copies each 32-key K/V
     // tile once into LDS, straight from the cache (global_load_lds), NSTAGE tiles deep: the
-    // copies of tiles i + 1 and i + 2 are in flight while tile i is used. Keys are the tile's
-    // 32 x D rows and values its [D][32] sub-tile, both with their 16-byte chunks permuted
-    // per row (chunk c of key row r at c ^ key_swizzle(r), of value row d at
+    // copies of tiles i + 1 and i + 2 are in flight while tile i is used. Keys are copied as
+    // stored (operand order: each operand read is 1 KiB of consecutive LDS), values as the
+    // tile's [D][32] sub-tile with the 16-byte chunks of row d permuted (chunk c at
     // c ^ ((d >> 2) & 3)) so that the fragment reads below hit distinct LDS banks.
     constexpr int KB = 32 * D * 2;              // key bytes per tile
     constexpr int SB = KB + D * 32 * 2;         // key and value bytes per tile
@@ -235,9 +235,6 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     constexpr int CP = SB / (kThreads * 16);    // 16-byte copies per lane per tile
     static_assert(SB % (kThreads * 16) == 0 && KB % (kThreads * 16) == 0, "attention tile copies");
     const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)smem);
-    auto key_swizzle = [](int r) {
-      return D >= 128 ? (r & 3) | (((r >> 3) & 3) << 2) : ((r >> 1) & 1) | (((r >> 3) & 3) << 1);
-    };
     const int tiles = (w.key_end - w.key_begin + 31) / 32;
     // Block-table entries of the range, one per lane, 64 blocks at a time: a table read
     // inside the pipelined loop would be a vector load (the copies clobber memory as far as
@@ -258,8 +255,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
         const int piece = q * (kThreads / 64) + wave;
         const int p = piece * 1024 + lane * 16;  // this lane's byte in the stage
         if (q * (kThreads / 64) * 1024 < KB) {
-          const int r = p / (2 * D), c = (p % (2 * D)) / 16;
-          lds_copy16(kb, (uint32_t)(r * 2 * D + ((c ^ key_swizzle(r)) * 16)), stage + piece * 1024);
+          lds_copy16(kb, (uint32_t)p, stage + piece * 1024);
         } else {
           const int d = (p - KB) / 64, c = ((p - KB) % 64) / 16;
           lds_copy16(vb, (uint32_t)(d * 64 + ((c ^ ((d >> 2) & 3)) * 16)), stage + piece * 1024);
@@ -269,12 +265,11 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     auto read_tile = [&](int buffer, Tile& f) {
       const char* ks = reinterpret_cast<const char*>(smem) + buffer * SB;
       const char* vs = ks + KB;
-      const int r0 = 8 * (col >> 2) + (col & 3);  // the permuted key rows of fetch()
+      const int lane16 = (threadIdx.x & 63) * 16;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const int c = 4 * kk + quad;
-        f.k0[kk] = *reinterpret_cast<const half8*>(ks + r0 * 2 * D + ((c ^ key_swizzle(r0)) * 16));
-        f.k1[kk] = *reinterpret_cast<const half8*>(ks + (r0 + 4) * 2 * D + ((c ^ key_swizzle(r0 + 4)) * 16));
+        f.k0[kk] = *reinterpret_cast<const half8*>(ks + (2 * kk) * 1024 + lane16);
+        f.k1[kk] = *reinterpret_cast<const half8*>(ks + (2 * kk + 1) * 1024 + lane16);
       }
 #pragma unroll
       for (int df = 0; df < DF; ++df) {

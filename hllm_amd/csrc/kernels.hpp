@@ -93,7 +93,8 @@ struct PackOut {
 };
 
 // Paged KV pool: [layers][blocks][K, V][kv_heads][...] with keys as [block_tokens][head_dim]
-// (a position's key contiguous) and values transposed in 32-position sub-tiles as
+// (a position's key contiguous; for the MFMA attention, 32-position tiles in operand order,
+// see kv_key_index) and values transposed in 32-position sub-tiles as
 // [block_tokens / 32][head_dim][32] (a dimension's values over 32 positions contiguous, and
 // one 32-key attention tile's values one contiguous region): the operand layouts of the
 // attention MFMAs. Blocks hold a multiple of 32 tokens.
@@ -104,11 +105,20 @@ struct KvView {
   int32_t kv_heads;
   int32_t head_dim;
   int32_t f32;             // element type: 1 = F32, 0 = F16
+  int32_t key_fragments;   // 1: each 32-position key tile in MFMA operand order (below)
 };
+// Keys of a block and head: [block_tokens][head_dim], or with key_fragments, per 32-position
+// tile the A operands of v_mfma_f32_16x16x32_f16 one after another: operand (kk, h) (dims
+// 32 kk .. 32 kk + 31 of rows 8 (c >> 2) + (c & 3) + 4 h, c = 0..15) is 1 KiB, lane
+// 16 q + c holding dims 32 kk + 8 q .. + 7 of its row, so that one operand is one contiguous
+// 1 KiB load per wave.
 __host__ __device__ inline uint64_t kv_key_index(const KvView& kv, int layer, uint64_t block, int offset,
                                                  int head, int d) {
-  return (uint64_t)layer * kv.layer_stride +
-         ((block * 2 * kv.kv_heads + head) * kv.block_tokens + offset) * kv.head_dim + d;
+  const uint64_t head_base = (uint64_t)layer * kv.layer_stride + (block * 2 * kv.kv_heads + head) * kv.block_tokens * kv.head_dim;
+  if (!kv.key_fragments) return head_base + (uint64_t)offset * kv.head_dim + d;
+  const int r = offset & 31, h = (r >> 2) & 1, c = ((r >> 3) << 2) | (r & 3);
+  return head_base + (uint64_t)(offset & ~31) * kv.head_dim +
+         (uint64_t)((((d >> 5) * 2 + h) * 64 + ((d >> 3) & 3) * 16 + c) * 8 + (d & 7));
 }
 __host__ __device__ inline uint64_t kv_value_index(const KvView& kv, int layer, uint64_t block, int offset,
                                                    int head, int d) {

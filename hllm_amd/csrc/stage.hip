@@ -486,6 +486,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   kv_.kv_heads = (int)K_;
   kv_.head_dim = (int)D_;
   kv_.f32 = kv_f32_ ? 1 : 0;
+  kv_.key_fragments = attention_uses_mfma((int)D_, kv_f32_) ? 1 : 0;
   kv_.layer_stride = blocks_total_ * 2 * K_ * bt * D_;
   free_blocks_.reserve(blocks_total_);
   for (uint64_t b = blocks_total_; b-- > 0;) free_blocks_.push_back((int32_t)b);
@@ -781,10 +782,10 @@ void Stage::read_kv(uint32_t handle, uint32_t layer, float* keys, float* values)
       for (uint64_t which = 0; which < 2; ++which)
         for (uint64_t hd = 0; hd < K_; ++hd)
           for (uint64_t d = 0; d < D_; ++d) {
-            // keys [head][position][dim]; values [head][position / 32][dim][position % 32]
-            const uint64_t o = p - p0;
-            const uint64_t i = which ? (K_ + hd) * head_elems + ((o >> 5) * D_ + d) * 32 + (o & 31)
-                                     : (hd * bt + o) * D_ + d;
+            // the block's elements as laid out by kv_key_index / kv_value_index
+            const int o = (int)(p - p0);
+            const uint64_t i = which ? kv_value_index(kv_, 0, 0, o, (int)hd, (int)d)
+                                     : kv_key_index(kv_, 0, 0, o, (int)hd, (int)d);
             float v;
             if (kv_f32_) {
               std::memcpy(&v, block.data() + i * 4, 4);
