@@ -448,7 +448,7 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     pack_.attn_max_splits = kMaxSplits;
     // Keys per split of decode-like attention blocks; HLLM_ROCM_ATTN_DECODE_SPLIT overrides
     // it for tuning (a multiple of 32).
-    pack_.attn_decode_unit = 384;
+    pack_.attn_decode_unit = 512;
     if (const char* v = std::getenv("HLLM_ROCM_ATTN_DECODE_SPLIT")) {
       const int unit = std::atoi(v);
       if (unit < 32 || unit % 32) fail(HLLM_INVALID_REQUEST, "HLLM_ROCM_ATTN_DECODE_SPLIT must be a multiple of 32");
