@@ -201,14 +201,21 @@ class Stage {
 
   // workspaces
   DeviceMemory h_, a0_hi_, a0_lo_, a1_hi_, a1_lo_, qkv_, q_, attn_partial_;
-  DeviceMemory gemm_ws_, gemm_counters_, logits_, argmax_val_, argmax_idx_, tokens_, flags_;
-  DeviceMemory items_dev_, host_tokens_dev_, pack_buf_, boundary_dev_, staging_, attn_work_;
+  // Per-pass inputs and outputs share one copy each way: items_dev_ holds the item list, then
+  // the input tokens; tokens_ the sampled tokens, then the pass's error flags.
+  DeviceMemory gemm_ws_, gemm_counters_, logits_, argmax_val_, argmax_idx_, tokens_;
+  DeviceMemory items_dev_, pack_buf_, boundary_dev_, staging_, attn_work_;
   bool mfma_attention_ = false;
   uint64_t attn_work_max_ = 0;
   size_t gemm_ws_floats_ = 0;
   int gemm_counter_count_ = 0;
   PackOut pack_{};
-  PinnedMemory pin_items_, pin_tokens_, pin_out_tokens_, pin_flags_, pin_boundary_;
+  PinnedMemory pin_items_, pin_out_tokens_, pin_boundary_;
+  size_t tokens_offset() const { return items_max_ * sizeof(ItemMeta); }
+  int32_t* host_tokens_dev() const { return reinterpret_cast<int32_t*>(static_cast<char*>(items_dev_.ptr) + tokens_offset()); }
+  int32_t* pin_tokens() const { return reinterpret_cast<int32_t*>(static_cast<char*>(pin_items_.ptr) + tokens_offset()); }
+  int32_t* flags_dev() const { return tokens_.as<int32_t>() + items_max_; }
+  int32_t* pin_flags() const { return pin_out_tokens_.as<int32_t>() + items_max_; }
   // sampler: per-row options, outputs [logprob: items][top values: items * 5][top IDs: items * 5]
   DeviceMemory sample_params_, sample_out_, sample_weights_, sample_lists_, sample_buckets_, sample_hist_,
       sample_lse_, sample_sorted_, sample_cursor_, sample_candidates_;
@@ -408,11 +415,9 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     HIP_CHECK(hipMemsetAsync(sample_hist_.ptr, 0, sample_hist_.bytes, stream_));
     HIP_CHECK(hipMemsetAsync(sample_cursor_.ptr, 0, sample_cursor_.bytes, stream_));
   }
-  tokens_.allocate(items_max_ * sizeof(int32_t), "tokens");
-  flags_.allocate(sizeof(int32_t), "flags");
-  pack_.flags = flags_.as<int32_t>();
-  items_dev_.allocate(items_max_ * sizeof(ItemMeta), "items");
-  host_tokens_dev_.allocate(R * sizeof(int32_t), "tokens");
+  tokens_.allocate((items_max_ + 1) * sizeof(int32_t), "tokens");
+  pack_.flags = flags_dev();
+  items_dev_.allocate(tokens_offset() + R * sizeof(int32_t), "items");
   pack_buf_.allocate(((items_max_ + 1) + 5 * R + 2 * items_max_ + 1) * sizeof(int32_t), "pack");
   {
     int32_t* p = pack_buf_.as<int32_t>();
@@ -456,12 +461,10 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     }
   }
   if (!c.first_stage || !c.final_stage) boundary_dev_.allocate(R * H_ * 2, "boundary");
-  pin_items_.allocate(items_max_ * sizeof(ItemMeta));
-  pin_tokens_.allocate(R * sizeof(int32_t));
-  pin_out_tokens_.allocate(items_max_ * sizeof(int32_t));
+  pin_items_.allocate(tokens_offset() + R * sizeof(int32_t));
+  pin_out_tokens_.allocate((items_max_ + 1) * sizeof(int32_t));
   pin_sample_params_.allocate(items_max_ * sizeof(SampleParams));
   pin_sample_out_.allocate(items_max_ * (6 * sizeof(double) + 5 * sizeof(int32_t)));
-  pin_flags_.allocate(sizeof(int32_t));
   pin_boundary_.allocate(R * H_ * 2);
   staging_.allocate(kStagingBytes, "load staging");
 
@@ -554,9 +557,9 @@ Target& Stage::target(const std::string& name) {
 
 void Stage::read_flags(const char* context) {
   int32_t flags = 0;
-  HIP_CHECK(hipMemcpyAsync(pin_flags_.ptr, flags_.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipMemcpyAsync(pin_flags(), flags_dev(), sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));
-  flags = *pin_flags_.as<int32_t>();
+  flags = *pin_flags();
   if (flags & 1) fail(HLLM_INCOMPATIBLE_WORKER, std::string("non-finite weight: ") + context);
   if (flags & 4) fail(HLLM_INCOMPATIBLE_WORKER, std::string("weight is not representable as finite F16: ") + context);
 }
@@ -575,7 +578,7 @@ void Stage::relayout(Target& t, const std::string& name, const void* device_src,
   a.row_base = row_base;
   a.cols = t.shape.size() == 2 ? t.shape[1] : t.shape[0];
   a.f16_resident = w_f32_ ? 0 : 1;
-  a.flags = flags_.as<int32_t>();
+  a.flags = flags_dev();
   if (t.matrix) {
     a.dst_hi = t.matrix->hi.as<uint16_t>();
     a.dst_lo = w_f32_ ? t.matrix->lo.as<uint16_t>() : nullptr;
@@ -603,7 +606,7 @@ void Stage::load_tensor(const std::string& name, uint32_t dtype, const uint64_t*
   const uint64_t rows = t.shape.size() == 2 ? t.shape[0] : 1;
   const uint64_t cols = t.shape.size() == 2 ? t.shape[1] : t.shape[0];
   if (bytes != rows * cols * el || !data) fail(HLLM_INCOMPATIBLE_WORKER, "truncated weight payload: " + name);
-  HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
+  HIP_CHECK(hipMemsetAsync(flags_dev(), 0, sizeof(int32_t), stream_));
   const uint64_t row_bytes = cols * el;
   const uint64_t chunk_rows = std::max<uint64_t>(1, kStagingBytes / row_bytes);
   if (row_bytes > kStagingBytes) fail(HLLM_INCOMPATIBLE_WORKER, "tensor row too large: " + name);
@@ -624,7 +627,7 @@ void Stage::synthesize(const std::string& name, uint64_t seed, uint64_t tensor_i
   Target& t = target(name);
   if (source_dtype != HLLM_DTYPE_F32 && source_dtype != HLLM_DTYPE_F16)
     fail(HLLM_INVALID_REQUEST, "synthetic source dtype must be F32 or F16");
-  HIP_CHECK(hipMemsetAsync(flags_.ptr, 0, sizeof(int32_t), stream_));
+  HIP_CHECK(hipMemsetAsync(flags_dev(), 0, sizeof(int32_t), stream_));
   const uint64_t rows = t.shape.size() == 2 ? t.shape[0] : 1;
   relayout(t, name, nullptr, source_dtype, seed, tensor_id, mean, sigma, 0, rows);
   read_flags(name.c_str());
@@ -1034,7 +1037,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   if (c_.first_stage && !pass.token_ids) fail(HLLM_INVALID_REQUEST, "stage zero requires tokens");
   if (!c_.first_stage && !pass.boundary_in) fail(HLLM_INVALID_REQUEST, "only stage zero accepts tokens");
   ItemMeta* meta = pin_items_.as<ItemMeta>();
-  int32_t* host_tokens = pin_tokens_.as<int32_t>();
+  int32_t* host_tokens = pin_tokens();
   {
     uint64_t r = 0;
     for (uint32_t i = 0; i < n; ++i) {
@@ -1094,12 +1097,11 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   // items of different lengths.
   const int attn_grid = attn_work_count;
   auto enqueue = [&](bool capturing) {
-    HIP_CHECK(hipMemcpyAsync(items_dev_.ptr, meta, n * sizeof(ItemMeta), hipMemcpyHostToDevice, stream_));
-    if (c_.first_stage)
-      HIP_CHECK(hipMemcpyAsync(host_tokens_dev_.ptr, host_tokens, R * sizeof(int32_t), hipMemcpyHostToDevice,
-                               stream_));
+    // The item list (all slots) and, on the first stage, the pass's tokens: one copy.
+    HIP_CHECK(hipMemcpyAsync(items_dev_.ptr, meta, tokens_offset() + (c_.first_stage ? R * sizeof(int32_t) : 0),
+                             hipMemcpyHostToDevice, stream_));
     timed("pack", 0, 0.0, [&] {
-      launch_pack(stream_, items_dev_.as<ItemMeta>(), (int)n, host_tokens_dev_.as<int32_t>(),
+      launch_pack(stream_, items_dev_.as<ItemMeta>(), (int)n, host_tokens_dev(),
                   last_token_.as<int32_t>(), block_table_.as<int32_t>(), table_width_, kv_.block_tokens, pack_);
     });
     float* h = h_.as<float>();
@@ -1200,7 +1202,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
              nullptr, 0);
         timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
           launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
-                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_.as<int32_t>());
+                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev());
         });
         if (sampler) {
           HIP_CHECK(hipMemcpyAsync(sample_params_.ptr, pin_sample_params_.ptr, S * sizeof(SampleParams),
@@ -1231,20 +1233,23 @@ void Stage::submit(const hllm_rocm_pass& pass) {
         }
         launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
                              items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
-        HIP_CHECK(hipMemcpyAsync(pin_out_tokens_.ptr, tokens_.ptr, S * sizeof(int32_t), hipMemcpyDeviceToHost,
-                                 stream_));
         if (pass.logits)
           HIP_CHECK(hipMemcpyAsync(pass.logits, logits_.ptr, (size_t)S * V_ * sizeof(float),
                                    hipMemcpyDeviceToHost, stream_));
       }
     } else {
       timed("boundary", (uint64_t)R * H_ * 6, 0.0, [&] {
-        launch_boundary_encode(stream_, h, R, (int)H_, boundary_dev_.as<uint16_t>(), flags_.as<int32_t>());
+        launch_boundary_encode(stream_, h, R, (int)H_, boundary_dev_.as<uint16_t>(), flags_dev());
       });
       HIP_CHECK(hipMemcpyAsync(pin_boundary_.ptr, boundary_dev_.ptr, (size_t)R * H_ * 2, hipMemcpyDeviceToHost,
                                stream_));
     }
-    HIP_CHECK(hipMemcpyAsync(pin_flags_.ptr, flags_.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
+    // The sampled tokens (final stage) and the error flags behind them: one copy.
+    if (c_.final_stage && S > 0)
+      HIP_CHECK(hipMemcpyAsync(pin_out_tokens_.ptr, tokens_.ptr, (items_max_ + 1) * sizeof(int32_t),
+                               hipMemcpyDeviceToHost, stream_));
+    else
+      HIP_CHECK(hipMemcpyAsync(pin_flags(), flags_dev(), sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
     HIP_CHECK(hipGetLastError());
   };
   try {
@@ -1319,7 +1324,7 @@ void Stage::wait() {
     fail_pass(pending_sequences_);
     check_hip(e, "pass");
   }
-  const int32_t flags = *pin_flags_.as<int32_t>();
+  const int32_t flags = *pin_flags();
   if (flags & 2) {
     fail_pass(pending_sequences_);
     fail(HLLM_INTERNAL, "cannot sample nonfinite logits");
