@@ -241,15 +241,23 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     // the compiler knows), and waiting for it would drain the copies in flight.
     const int last_block = (w.key_end - 1) / bt;
     int held_base = 0, held = 0;
-    // This wave's copies of tile i into stage i % NSTAGE: wave-sized 1 KiB pieces of the
-    // stage, interleaved over the waves, the first KB / 1024 of them keys.
-    auto issue = [&](int i) {
-      const int t = w.key_begin + 32 * i;
-      const uint64_t blk = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(held, t / bt - held_base);
-      const int off = t % bt;
-      const _Float16* kb = pool + ((blk * 2 * KVH + kvh) * bt + off) * D;
-      const _Float16* vb = pool + ((blk * 2 + 1) * KVH + kvh) * (uint64_t)bt * D + (uint64_t)(off >> 5) * D * 32;
-      const uint32_t stage = lds_base + (uint32_t)(i % NSTAGE) * SB;
+    // Copy-side state, advanced once per issued tile so that no division or modulo runs in
+    // the loop (scalar instructions are shared by the CU's waves): the next tile's block
+    // (relative to held_base), its offset in the block and its stage's LDS offset.
+    int rel = 0, off = 0;
+    uint32_t next_stage = 0;
+    const _Float16* key_base = pool + (uint64_t)kvh * bt * D;
+    const _Float16* value_base = pool + (uint64_t)(KVH + kvh) * bt * D;
+    const uint64_t block_elems = (uint64_t)2 * KVH * bt * D;
+    // This wave's copies of the next tile into its stage: wave-sized 1 KiB pieces of the
+    // stage, interleaved over the waves, the first KB / 1024 of them keys. A tile's values
+    // start off * D elements into the block's value region, as its keys do (off is a
+    // multiple of 32).
+    auto issue = [&]() {
+      const uint64_t at = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(held, rel) * block_elems + (uint64_t)off * D;
+      const _Float16* kb = key_base + at;
+      const _Float16* vb = value_base + at;
+      const uint32_t stage = lds_base + next_stage;
 #pragma unroll
       for (int q = 0; q < CP; ++q) {
         const int piece = q * (kThreads / 64) + wave;
@@ -261,9 +269,15 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
           lds_copy16(vb, (uint32_t)(d * 64 + ((c ^ ((d >> 2) & 3)) * 16)), stage + piece * 1024);
         }
       }
+      off += 32;
+      if (off == bt) {
+        off = 0;
+        ++rel;
+      }
+      next_stage = next_stage == (NSTAGE - 1) * SB ? 0 : next_stage + SB;
     };
-    auto read_tile = [&](int buffer, Tile& f) {
-      const char* ks = reinterpret_cast<const char*>(smem) + buffer * SB;
+    auto read_tile = [&](uint32_t stage_offset, Tile& f) {
+      const char* ks = reinterpret_cast<const char*>(smem) + stage_offset;
       const char* vs = ks + KB;
       const int lane16 = (threadIdx.x & 63) * 16;
 #pragma unroll
@@ -277,14 +291,17 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
         f.v[df] = *reinterpret_cast<const half8*>(vs + d * 64 + ((quad ^ ((d >> 2) & 3)) * 16));
       }
     };
+    uint32_t read_stage = 0;
     for (int i0 = 0; i0 < tiles;) {
       // Tiles [i0, i1) lie in the 64 blocks held from held_base; the pipeline restarts
       // after each such group (ranges of more than 64 blocks only).
       held_base = (w.key_begin + 32 * i0) / bt;
       held = table[min(held_base + lane, last_block)];
+      rel = 0;
+      off = (w.key_begin + 32 * i0) % bt;
       const int i1 = min(tiles, ((held_base + 64) * bt - w.key_begin) / 32);
-      issue(i0);
-      if (i0 + 1 < i1) issue(i0 + 1);
+      issue();
+      if (i0 + 1 < i1) issue();
       for (int i = i0; i < i1; ++i) {
         // Tile i has landed once this wave's later copies (tile i + 1's) are all that is
         // outstanding and every wave has got here; that also means every wave is done
@@ -293,9 +310,10 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
           stage_barrier<CP, 0>();
         else
           stage_barrier<0, 0>();
-        if (i + 2 < i1) issue(i + 2);  // workgroup-uniform
+        if (i + 2 < i1) issue();  // tile i + 2; workgroup-uniform
         Tile f;
-        read_tile(i % NSTAGE, f);
+        read_tile(read_stage, f);
+        read_stage = read_stage == (NSTAGE - 1) * SB ? 0 : read_stage + SB;
         consume(w.key_begin + 32 * i, f);
       }
       i0 = i1;
