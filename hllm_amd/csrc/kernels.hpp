@@ -35,7 +35,7 @@ __host__ __device__ inline int attn_block_rows(int group) { return group >= 64 ?
 constexpr int kAttnPrefillUnit = 1024;
 
 // Splits of a block's `keys` key positions, 32-key aligned and non-empty: every
-// `decode_unit` keys (a multiple of 32; 256 by default) for decode-like blocks (at most 16
+// `decode_unit` keys (a multiple of 32; 512 by default) for decode-like blocks (at most 16
 // query vectors: the workgroup's four waves share the keys, and short splits balance rows
 // of very different context lengths), every kAttnPrefillUnit keys for prefill blocks.
 __host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits, int decode_unit) {
