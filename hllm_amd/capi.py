@@ -30,7 +30,7 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
            "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
            "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config",
-           "hllm_rocm_measure_read_bandwidth")
+           "hllm_rocm_measure_read_bandwidth", "hllm_rocm_stage_execute_profiled")
 
 
 class StageError(RuntimeError):
@@ -72,6 +72,10 @@ class Pass(C.Structure):
                 ("trace_hidden", C.POINTER(C.c_float))]
 
 
+class PhaseTime(C.Structure):
+    _fields_ = [("component", C.c_char * 16), ("layer", C.c_int32), ("milliseconds", C.c_double)]
+
+
 class Memory(C.Structure):
     _fields_ = [("host_bytes", C.c_uint64), ("device_bytes", C.c_uint64),
                 ("pinned_host_bytes", C.c_uint64), ("unified_bytes", C.c_uint64)]
@@ -107,6 +111,8 @@ def library() -> C.CDLL:
     L.hllm_rocm_stage_execute.argtypes = [vp, C.POINTER(Pass)]
     L.hllm_rocm_stage_submit.argtypes = [vp, C.POINTER(Pass)]
     L.hllm_rocm_stage_wait.argtypes = [vp]
+    L.hllm_rocm_stage_execute_profiled.argtypes = [vp, C.POINTER(Pass), C.POINTER(PhaseTime), u32,
+                                                   C.POINTER(u32)]
     L.hllm_rocm_stage_last_layout.argtypes = [vp, u32, u32, C.POINTER(C.c_int32),
                                               C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
     L.hllm_rocm_sequence_blocks.argtypes = [vp, u32, C.POINTER(C.c_int32), u32, C.POINTER(u32),
@@ -293,6 +299,33 @@ class Stage:
         check(self.lib.hllm_rocm_stage_execute(self.handle, C.byref(p)))
         del keep
         return out
+
+    def execute_profiled(self, items, token_ids=None, boundary=None, want_logits=False,
+                         cancelled=None):
+        """execute() plus per-phase device times: out["phases"] = [(component, layer or None,
+        milliseconds)] (runtime::ExecutionTiming)."""
+        p, out, keep = self.make_pass(items, token_ids, boundary, want_logits, False, cancelled)
+        c = self.config
+        capacity = (c.layer_end - c.layer_start) + 8
+        phases = (PhaseTime * capacity)()
+        count = C.c_uint32(0)
+        check(self.lib.hllm_rocm_stage_execute_profiled(self.handle, C.byref(p), phases, capacity,
+                                                        C.byref(count)))
+        del keep
+        out["phases"] = [(phases[i].component.decode(), None if phases[i].layer < 0 else phases[i].layer,
+                          phases[i].milliseconds) for i in range(min(count.value, capacity))]
+        return out
+
+    def submit(self, items, token_ids=None, boundary=None, want_logits=False, cancelled=None):
+        """Enqueue a pass without waiting: returns a handle for wait()."""
+        p, out, keep = self.make_pass(items, token_ids, boundary, want_logits, False, cancelled)
+        check(self.lib.hllm_rocm_stage_submit(self.handle, C.byref(p)))
+        return (p, out, keep)
+
+    def wait(self, handle):
+        """Completes the submitted pass; returns its outputs."""
+        check(self.lib.hllm_rocm_stage_wait(self.handle))
+        return handle[1]
 
     # --------------------------------------------------------------- graphs
     def set_graphs(self, enabled: bool) -> None:

@@ -152,6 +152,11 @@ struct Partials {
 // gathered through `row_index` (nullptr = identity) with `count` read from device
 // memory when `device_rows` is non-null. With `residual` partials (identity rows only)
 // the row is first updated in place: h += sum of the partials.
+// h += the partials summed in split order from zero: the residual update the RMSNorm
+// kernel makes with `residual` partials, with the same additions, for passes that read the
+// residual stream between layers (traces).
+void launch_residual_sum(hipStream_t stream, float* h, int rows, int hidden, Partials residual);
+
 void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int32_t* row_index,
                             int rows, const int32_t* device_rows, const float* weight, float eps,
                             uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,

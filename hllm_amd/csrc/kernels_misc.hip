@@ -614,6 +614,22 @@ void launch_boundary_encode(hipStream_t stream, const float* h, int rows, int hi
                                                                                       flags); });
 }
 
+__global__ void __launch_bounds__(256) residual_sum_kernel(float* h, int64_t elements, Partials residual) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= elements) return;
+  float y = 0.0f;
+  for (int s = 0; s < residual.parts; ++s) y += residual.data[(size_t)s * residual.stride + e];
+  h[e] += y;
+}
+
+void launch_residual_sum(hipStream_t stream, float* h, int rows, int hidden, Partials residual) {
+  if (rows <= 0 || residual.parts <= 0) return;
+  const int64_t elements = (int64_t)rows * hidden;
+  observed("residual_sum_kernel", [&] {
+    residual_sum_kernel<<<(unsigned)((elements + 255) / 256), 256, 0, stream>>>(h, elements, residual);
+  });
+}
+
 void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int32_t* row_index,
                             int rows, const int32_t* device_rows, const float* weight, float eps,
                             uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,

@@ -84,9 +84,25 @@ struct Layer {
 struct Sequence {
   bool live = false;
   bool failed = false;
+  // The sequence's previous pass sampled a token, which the device holds for a
+  // device-fed input of its next pass.
+  bool device_token = false;
+  // A submitted pass uses the sequence (its KV blocks must not be handed out again).
+  bool in_flight = false;
+  // Released while in flight: the slot and blocks return to the pools when the pass completes.
+  bool release_pending = false;
   uint64_t capacity = 0;
   uint64_t length = 0;
   std::vector<int32_t> blocks;
+};
+
+// Per-phase timing of a profiled pass (runtime::ExecutionTiming components,
+// cpp/include/hllm/runtime/timing.hpp:11-18): events recorded on the stage's stream
+// between phases, read once the pass completes.
+struct PhaseMark {
+  const char* component;
+  int32_t layer;  // -1: not a layer
+  hipEvent_t end;
 };
 
 // Expected tensor: shape and where it goes.
@@ -133,8 +149,8 @@ class Stage {
   uint32_t allocate_sequence(uint64_t tokens);
   void release_sequence(uint32_t handle);
   uint64_t sequence_length(uint32_t handle) const;
-  void submit(const hllm_rocm_pass& pass);
-  void wait();
+  void submit(const hllm_rocm_pass& pass, bool phases = false);
+  void wait(hllm_rocm_phase_time* phases = nullptr, uint32_t capacity = 0, uint32_t* count = nullptr);
   void last_layout(uint32_t items, uint32_t rows, int32_t* cu, int32_t* pos, int32_t* slots);
   void sequence_blocks(uint32_t handle, int32_t* blocks, uint32_t capacity, uint32_t* count,
                        uint32_t* block_tokens);
@@ -168,6 +184,11 @@ class Stage {
   void timed(const char* family, uint64_t bytes, double flops, F&& launch);
   hipEvent_t take_event();
   void fail_pass(const std::vector<uint32_t>& sequences);
+  // Ends the in-flight use of a pass's sequences (under seq_mutex_): clears the flag and
+  // returns the slots and blocks of sequences released meanwhile.
+  void retire_sequences(const std::vector<uint32_t>& sequences);
+  void free_sequence(uint32_t handle);
+  void mark_phase(const char* component, int32_t layer);
 
   hllm_rocm_stage_config c_;
   int device_ = 0;
@@ -255,6 +276,10 @@ class Stage {
   std::vector<int> pending_top_counts_;  // per sampled row: -1 without log-probabilities
   bool pending_sampler_ = false;
   uint64_t pending_rows_ = 0;
+  // execute_profiled: the pass's start event and one mark per completed phase.
+  bool phases_on_ = false;
+  hipEvent_t phase_start_ = nullptr;
+  std::vector<PhaseMark> phase_marks_;
 
   bool profiling_ = false;
   std::vector<std::string> profile_filter_;
@@ -510,7 +535,10 @@ Stage::~Stage() {
       (void)hipGraphDestroy(g.graph);
     }
     for (auto& [name, p] : profiles_)
-      for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
+      if (p.owns_events)
+        for (auto& e : p.events) event_pool_.push_back(e.first), event_pool_.push_back(e.second);
+    for (const PhaseMark& m : phase_marks_) event_pool_.push_back(m.end);
+    if (phase_start_) event_pool_.push_back(phase_start_);
     for (auto e : event_pool_) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(stream_);
   }
@@ -682,18 +710,43 @@ uint32_t Stage::allocate_sequence(uint64_t tokens) {
   free_slots_.pop_back();
   s.live = true;
   s.failed = false;
+  s.device_token = false;
+  s.in_flight = false;
+  s.release_pending = false;
   s.capacity = tokens;
   s.length = 0;
   return slot;
 }
 
-void Stage::release_sequence(uint32_t handle) {
-  std::lock_guard<std::mutex> lock(seq_mutex_);
-  if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+void Stage::free_sequence(uint32_t handle) {
   Sequence& s = sequences_[handle];
   free_blocks_.insert(free_blocks_.end(), s.blocks.begin(), s.blocks.end());
   s = Sequence{};
   free_slots_.push_back(handle);
+}
+
+// SequenceState destruction may run while a pass that uses the sequence is in flight
+// (cpp/src/worker/control_service.cpp:509-530): the handle is invalid at once, but its slot
+// and KV blocks return to the pools only when that pass completes, so no later sequence
+// inherits the pass's state or shares blocks the device is still writing.
+void Stage::release_sequence(uint32_t handle) {
+  std::lock_guard<std::mutex> lock(seq_mutex_);
+  if (handle >= sequences_.size() || !sequences_[handle].live) fail(HLLM_INVALID_REQUEST, "unknown sequence");
+  Sequence& s = sequences_[handle];
+  if (s.in_flight) {
+    s.live = false;
+    s.release_pending = true;
+    return;
+  }
+  free_sequence(handle);
+}
+
+void Stage::retire_sequences(const std::vector<uint32_t>& sequences) {
+  for (uint32_t h : sequences) {
+    Sequence& s = sequences_[h];
+    s.in_flight = false;
+    if (s.release_pending) free_sequence(h);
+  }
 }
 
 uint64_t Stage::sequence_length(uint32_t handle) const {
@@ -984,54 +1037,62 @@ int Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const
   return parts;
 }
 
+// A pass that failed after its work was enqueued: the device may have written part of the
+// sequences' KV, so they are never resumed (cpp/src/cuda/stage.cpp:463-468), and their
+// in-flight use ends here.
 void Stage::fail_pass(const std::vector<uint32_t>& sequences) {
   (void)hipStreamSynchronize(stream_);
   std::lock_guard<std::mutex> lock(seq_mutex_);
-  for (uint32_t s : sequences)
-    if (s < sequences_.size()) sequences_[s].failed = true;
+  for (uint32_t s : sequences) {
+    sequences_[s].failed = true;
+    sequences_[s].device_token = false;
+  }
+  retire_sequences(sequences);
 }
 
-void Stage::submit(const hllm_rocm_pass& pass) {
+void Stage::mark_phase(const char* component, int32_t layer) {
+  if (!phases_on_) return;
+  hipEvent_t e = take_event();
+  HIP_CHECK(hipEventRecord(e, stream_));
+  phase_marks_.push_back({component, layer, e});
+}
+
+void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
   std::unique_lock<std::mutex> lock(pass_mutex_);
   if (!finalized_) fail(HLLM_INVALID_REQUEST, "stage is not finalized");
   if (in_flight_) fail(HLLM_INVALID_REQUEST, "a pass is already in flight");
   const uint32_t n = pass.items;
   if (n == 0 || n > items_max_ || !pass.item) fail(HLLM_INVALID_REQUEST, "invalid pass size");
-  // ---- validate on the host (positions, capacities, inputs) before touching the device
+  // ---- validate the request on the host (inputs first, then the sequences' state) before
+  // touching the device
   uint64_t rows = 0;
   std::vector<uint32_t> seqs(n);
   std::vector<int> sample_items;
   std::vector<int> top_counts;
   bool sampler = false;
   SampleParams* params = pin_sample_params_.as<SampleParams>();
-  {
-    std::lock_guard<std::mutex> sl(seq_mutex_);
-    std::set<uint32_t> unique;
-    for (uint32_t i = 0; i < n; ++i) {
-      const hllm_rocm_item& it = pass.item[i];
-      if (it.sequence >= sequences_.size() || !sequences_[it.sequence].live)
-        fail(HLLM_INVALID_REQUEST, "unknown sequence");
-      const Sequence& s = sequences_[it.sequence];
-      if (s.failed || it.first_position != s.length || it.query_tokens == 0 ||
-          it.query_tokens > s.capacity - std::min(s.capacity, s.length) ||
-          !unique.insert(it.sequence).second)
-        fail(HLLM_INVALID_REQUEST, "invalid sequence state, position or context capacity");
-      if ((it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) && (!c_.first_stage || it.query_tokens != 1 || s.length == 0))
-        fail(HLLM_INVALID_REQUEST, "device-fed input needs one token of a started sequence");
-      if (it.flags & HLLM_ITEM_SAMPLE) {
-        check_sampling(it);
-        if (c_.final_stage) {
-          const bool logprobs = (it.flags & HLLM_ITEM_LOGPROBS) != 0;
-          params[sample_items.size()] = {it.temperature, it.top_p, it.top_k, it.seed, it.generated_index,
-                                         logprobs ? it.top_logprobs : 0u, logprobs ? kSampleLogprobs : 0u};
-          sampler |= it.temperature != 0.0 || logprobs;
-          top_counts.push_back(logprobs ? (int)it.top_logprobs : -1);
-          sample_items.push_back((int)i);
-        }
+  for (uint32_t i = 0; i < n; ++i) {
+    const hllm_rocm_item& it = pass.item[i];
+    if (it.query_tokens == 0 || it.query_tokens > c_.maximum_sequence_length ||
+        it.first_position > c_.maximum_sequence_length)
+      fail(HLLM_INVALID_REQUEST, "invalid sequence state, position or context capacity");
+    // The device keeps the token sampled by the final stage, and only the first stage
+    // embeds tokens: device-fed inputs need a stage that is both.
+    if ((it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) && (!c_.first_stage || !c_.final_stage || it.query_tokens != 1))
+      fail(HLLM_INVALID_REQUEST, "device-fed input needs one token on a stage that embeds and samples");
+    if (it.flags & HLLM_ITEM_SAMPLE) {
+      check_sampling(it);
+      if (c_.final_stage) {
+        const bool logprobs = (it.flags & HLLM_ITEM_LOGPROBS) != 0;
+        params[sample_items.size()] = {it.temperature, it.top_p, it.top_k, it.seed, it.generated_index,
+                                       logprobs ? it.top_logprobs : 0u, logprobs ? kSampleLogprobs : 0u};
+        sampler |= it.temperature != 0.0 || logprobs;
+        top_counts.push_back(logprobs ? (int)it.top_logprobs : -1);
+        sample_items.push_back((int)i);
       }
-      seqs[i] = it.sequence;
-      rows += it.query_tokens;
     }
+    seqs[i] = it.sequence;
+    rows += it.query_tokens;
   }
   if (rows > rows_max_) fail(HLLM_RESOURCE_EXHAUSTED, "pass exceeds the stage's row budget");
   if (c_.first_stage && !pass.token_ids) fail(HLLM_INVALID_REQUEST, "stage zero requires tokens");
@@ -1116,6 +1177,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       timed("boundary", (uint64_t)R * H_ * 6, 0.0,
             [&] { launch_boundary_decode(stream_, boundary_dev_.as<uint16_t>(), R, (int)H_, h); });
     }
+    mark_phase(c_.first_stage ? "embedding" : "from-wire", -1);
     uint16_t* a0h = a0_hi_.as<uint16_t>();
     uint16_t* a0l = a0_lo_.as<uint16_t>();
     uint16_t* a1h = a1_hi_.as<uint16_t>();
@@ -1179,13 +1241,19 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       });
       gemm("gemm_gate_up", w.gate_up, a0h, a0l, R, (int)(2 * Ip_), kEpiSwiglu, nullptr, 0, a1h, a1l, Ip_);
       // The last layer's residual completes here (the final norm gathers sampled rows, and
-      // the boundary and trace read the whole stream).
-      const bool defer_down = l + 1 < L_ && !pass.trace_hidden;
+      // the boundary reads the whole stream).
+      const bool defer_down = l + 1 < L_;
       const int down_parts = gemm("gemm_down", w.down, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr,
                                   nullptr, 0, defer_down);
       pending = Partials{ws, down_parts, (uint64_t)R * H_};
       HIP_CHECK(hipGetLastError());
+      mark_phase("layer", (int32_t)(c_.layer_start + l));
       if (pass.trace_hidden) {
+        // The trace reads the completed residual stream: the pending partials are added
+        // here, with the additions the next norm would make, so a traced pass computes
+        // exactly what an untraced one does.
+        launch_residual_sum(stream_, h, R, (int)H_, pending);
+        pending = {};
         HIP_CHECK(hipMemcpyAsync(pass.trace_hidden + l * (size_t)R * H_, h, (size_t)R * H_ * sizeof(float),
                                  hipMemcpyDeviceToHost, stream_));
         HIP_CHECK(hipStreamSynchronize(stream_));
@@ -1197,9 +1265,11 @@ void Stage::submit(const hllm_rocm_pass& pass) {
           launch_rmsnorm_flayout(stream_, h, (int)H_, pack_.sample_row, S, nullptr, final_norm_.as<float>(), eps,
                                  a0h, a0l, Hp_);
         });
+        mark_phase("final_norm", -1);
         const Matrix& head = c_.tied_head ? embedding_ : head_;
         gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
              nullptr, 0);
+        mark_phase("lm_head", -1);
         timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
           launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
                         argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev());
@@ -1233,6 +1303,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
         }
         launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
                              items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
+        mark_phase("sampling", -1);
         if (pass.logits)
           HIP_CHECK(hipMemcpyAsync(pass.logits, logits_.ptr, (size_t)S * V_ * sizeof(float),
                                    hipMemcpyDeviceToHost, stream_));
@@ -1243,6 +1314,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       });
       HIP_CHECK(hipMemcpyAsync(pin_boundary_.ptr, boundary_dev_.ptr, (size_t)R * H_ * 2, hipMemcpyDeviceToHost,
                                stream_));
+      mark_phase("to-wire", -1);
     }
     // The sampled tokens (final stage) and the error flags behind them: one copy.
     if (c_.final_stage && S > 0)
@@ -1252,10 +1324,32 @@ void Stage::submit(const hllm_rocm_pass& pass) {
       HIP_CHECK(hipMemcpyAsync(pin_flags(), flags_dev(), sizeof(int32_t), hipMemcpyDeviceToHost, stream_));
     HIP_CHECK(hipGetLastError());
   };
+  // ---- the sequences' state, checked and claimed for this pass under one lock
+  {
+    std::lock_guard<std::mutex> sl(seq_mutex_);
+    std::set<uint32_t> unique;
+    for (uint32_t i = 0; i < n; ++i) {
+      const hllm_rocm_item& it = pass.item[i];
+      if (it.sequence >= sequences_.size() || !sequences_[it.sequence].live)
+        fail(HLLM_INVALID_REQUEST, "unknown sequence");
+      const Sequence& s = sequences_[it.sequence];
+      if (s.failed || it.first_position != s.length ||
+          it.query_tokens > s.capacity - std::min(s.capacity, s.length) || !unique.insert(it.sequence).second)
+        fail(HLLM_INVALID_REQUEST, "invalid sequence state, position or context capacity");
+      if ((it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) && !s.device_token)
+        fail(HLLM_INVALID_REQUEST, "device-fed input needs a token sampled by the sequence's previous pass");
+    }
+    for (uint32_t s : seqs) sequences_[s].in_flight = true;
+  }
+  phases_on_ = phases;
+  for (const PhaseMark& m : phase_marks_) event_pool_.push_back(m.end);
+  phase_marks_.clear();
+  if (phases && !phase_start_) phase_start_ = take_event();
   try {
+    if (phases) HIP_CHECK(hipEventRecord(phase_start_, stream_));
     const PassShape shape{n, (uint32_t)R, (uint32_t)S, sampler ? 1u : 0u, (uint32_t)attn_grid,
                           attn_any_split ? 1u : 0u};
-    const bool graphable = graphs_enabled_ && !profiling_ && !pass.logits && !pass.trace_hidden;
+    const bool graphable = graphs_enabled_ && !profiling_ && !phases && !pass.logits && !pass.trace_hidden;
     auto found = graphable ? graphs_.find(shape) : graphs_.end();
     if (found != graphs_.end()) {
       found->second.used = ++graph_clock_;
@@ -1315,7 +1409,7 @@ void Stage::submit(const hllm_rocm_pass& pass) {
   pending_rows_ = rows;
 }
 
-void Stage::wait() {
+void Stage::wait(hllm_rocm_phase_time* phases, uint32_t capacity, uint32_t* count) {
   std::unique_lock<std::mutex> lock(pass_mutex_);
   if (!in_flight_) fail(HLLM_INVALID_REQUEST, "no pass in flight");
   in_flight_ = false;
@@ -1323,6 +1417,33 @@ void Stage::wait() {
   if (e != hipSuccess) {
     fail_pass(pending_sequences_);
     check_hip(e, "pass");
+  }
+  // Cancellation is checked before each layer is enqueued and once more when the pass has
+  // completed, before the sequences advance (cpp/src/cuda/stage.cpp:396,456): a pass
+  // cancelled while it ran is discarded and its sequences are never resumed.
+  if (pending_.cancelled && *pending_.cancelled) {
+    fail_pass(pending_sequences_);
+    fail(HLLM_CANCELLED, "request cancelled");
+  }
+  if (count) *count = 0;
+  if (phases_on_) {
+    hipEvent_t previous = phase_start_;
+    uint32_t k = 0;
+    for (const PhaseMark& m : phase_marks_) {
+      float ms = 0.f;
+      HIP_CHECK(hipEventElapsedTime(&ms, previous, m.end));
+      previous = m.end;
+      if (phases && k < capacity) {
+        hllm_rocm_phase_time& t = phases[k];
+        std::memset(t.component, 0, sizeof(t.component));
+        std::strncpy(t.component, m.component, sizeof(t.component) - 1);
+        t.layer = m.layer;
+        t.milliseconds = ms;
+      }
+      ++k;
+    }
+    if (count) *count = k;
+    phases_on_ = false;
   }
   const int32_t flags = *pin_flags();
   if (flags & 2) {
@@ -1357,7 +1478,13 @@ void Stage::wait() {
   }
   if (!c_.final_stage && pass.boundary_out) std::memcpy(pass.boundary_out, pin_boundary_.ptr, pending_rows_ * H_ * 2);
   std::lock_guard<std::mutex> sl(seq_mutex_);
-  for (size_t i = 0; i < pending_sequences_.size(); ++i) sequences_[pending_sequences_[i]].length += pending_lengths_[i];
+  for (size_t i = 0; i < pending_sequences_.size(); ++i) {
+    Sequence& s = sequences_[pending_sequences_[i]];
+    s.length += pending_lengths_[i];
+    s.device_token = false;
+  }
+  for (int item : pending_sample_items_) sequences_[pending_sequences_[item]].device_token = true;
+  retire_sequences(pending_sequences_);
 }
 
 // The sampling options of one item, checked as runtime::validate_sampling
@@ -1625,6 +1752,16 @@ hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass
   const hllm_status s = hllm_rocm_stage_submit(stage, pass);
   if (s != HLLM_OK) return s;
   return hllm_rocm_stage_wait(stage);
+}
+
+hllm_status hllm_rocm_stage_execute_profiled(hllm_rocm_stage* stage, const hllm_rocm_pass* pass,
+                                             hllm_rocm_phase_time* phases, uint32_t capacity, uint32_t* count) {
+  const hllm_status s = guarded([&] {
+    if (!pass || !count || (capacity && !phases)) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null argument");
+    impl(stage).submit(*pass, true);
+  });
+  if (s != HLLM_OK) return s;
+  return guarded([&] { impl(stage).wait(phases, capacity, count); });
 }
 
 hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t vocabulary,

@@ -87,7 +87,8 @@ typedef struct {
  * only extends the KV cache: PrefillProgress, cpp/src/cpu/stage.cpp:164). */
 #define HLLM_ITEM_SAMPLE 1u
 /* The item's single input token is the token its sequence sampled in its previous pass,
- * read on the device (no host round trip). First stage only. */
+ * read on the device (no host round trip). Only on a stage that is both first and final,
+ * and only when the sequence's previous pass sampled (HLLM_INVALID_REQUEST otherwise). */
 #define HLLM_ITEM_TOKEN_FROM_DEVICE 2u
 /* Return log-probabilities (runtime::SampledToken, cpp/src/sampling.cpp:65-89). */
 #define HLLM_ITEM_LOGPROBS 4u
@@ -98,7 +99,12 @@ typedef struct {
   const hllm_rocm_item* item;
   const uint64_t* token_ids;     /* first stage: sum(query_tokens) IDs in item order */
   const uint16_t* boundary_in;   /* other stages: [sum(query_tokens), hidden] F16 LE */
-  const volatile int32_t* cancelled; /* optional; polled between layers */
+  /* Optional. Checked before the pass is enqueued, before each layer is enqueued, and once
+   * more when the pass completes (cpp/src/cuda/stage.cpp:357,396,456). Set before the
+   * device runs the pass, nothing changes; set while it runs, the pass's results are
+   * discarded, its sequences are failed (never resumed, cpp/src/cuda/stage.cpp:463-468)
+   * and the call returns HLLM_CANCELLED. */
+  const volatile int32_t* cancelled;
   /* outputs (host pointers; NULL = not wanted) */
   uint64_t* tokens;              /* final stage: [items]; items without SAMPLE get UINT64_MAX */
   /* For sampled items with HLLM_ITEM_LOGPROBS (runtime::SampledToken): the token's
@@ -143,14 +149,22 @@ hllm_status hllm_rocm_stage_synthesize_tensor(hllm_rocm_stage* stage, const char
 /* Verify that every owned tensor arrived; the stage accepts passes afterwards. */
 hllm_status hllm_rocm_stage_finalize(hllm_rocm_stage* stage);
 
-/* StageBackend::weight_memory / sequence_memory (stage_backend.hpp:72-83). */
+/* StageBackend::weight_memory / sequence_memory (stage_backend.hpp:72-83). With
+ * rows = query_rows(tokens, maximum_query_tokens) (stage_backend.hpp:62-67) and bt the KV
+ * block size: cache = {host: tokens * 24 + rows * hidden * 6 (request_transport_bytes,
+ * stage_backend.hpp:36-40), device: ceil(tokens / bt) * bt * layers * 2 * kv_heads *
+ * head_dim * (2 for F16 KV, 4 for F32 KV)}; workspace = {host: rows * hidden * 6 + 65536,
+ * device: 0} (pass workspaces are reserved when the stage is created). tokens = 0 or above
+ * maximum_sequence_length is HLLM_INVALID_REQUEST. */
 hllm_status hllm_rocm_stage_weight_memory(const hllm_rocm_stage* stage, hllm_rocm_memory* out);
 hllm_status hllm_rocm_stage_sequence_memory(const hllm_rocm_stage* stage, uint64_t tokens,
                                             uint64_t maximum_query_tokens,
                                             hllm_rocm_memory* cache, hllm_rocm_memory* workspace);
 
 /* StageBackend::allocate_sequence (stage_backend.hpp:84-85): reserve paged KV for `tokens`
- * positions; release returns the blocks (SequenceState destruction). */
+ * positions (HLLM_RESOURCE_EXHAUSTED when the block pool or the sequence slots run out).
+ * Release is SequenceState destruction: the handle is invalid at once; when a submitted pass
+ * still uses the sequence, its slot and blocks return to the pools when that pass completes. */
 hllm_status hllm_rocm_sequence_allocate(hllm_rocm_stage* stage, uint64_t tokens, uint32_t* sequence);
 hllm_status hllm_rocm_sequence_release(hllm_rocm_stage* stage, uint32_t sequence);
 hllm_status hllm_rocm_sequence_length(const hllm_rocm_stage* stage, uint32_t sequence,
@@ -166,6 +180,25 @@ hllm_status hllm_rocm_stage_execute(hllm_rocm_stage* stage, const hllm_rocm_pass
  * hllm_rocm_stage_wait. At most one pass is in flight per stage. */
 hllm_status hllm_rocm_stage_submit(hllm_rocm_stage* stage, const hllm_rocm_pass* pass);
 hllm_status hllm_rocm_stage_wait(hllm_rocm_stage* stage);
+
+/* One timed phase of a profiled pass: runtime::ComponentTiming
+ * (cpp/include/hllm/runtime/timing.hpp:11-15). Components, in pass order: "embedding" or
+ * "from-wire", "layer" (layer = its model layer index) per owned layer, then "final_norm",
+ * "lm_head" and "sampling" (final stage, when the pass samples) or "to-wire" (other
+ * stages); layer is -1 except for "layer". */
+typedef struct {
+  char component[16];
+  int32_t layer;
+  double milliseconds;
+} hllm_rocm_phase_time;
+
+/* StageBackend::execute_profiled (stage_backend.hpp:103-106): hllm_rocm_stage_execute with
+ * HIP events between phases on the stage's stream (no synchronisation inside the pass, so
+ * the outputs equal hllm_rocm_stage_execute's bit for bit). Writes up to `capacity` phases
+ * and their number to *count. */
+hllm_status hllm_rocm_stage_execute_profiled(hllm_rocm_stage* stage, const hllm_rocm_pass* pass,
+                                             hllm_rocm_phase_time* phases, uint32_t capacity,
+                                             uint32_t* count);
 
 /* runtime::sample_token (cpp/src/sampling.cpp:65-89) on the device for `rows` rows of
  * `vocabulary` F32 logits (host memory), each with the sampling fields of options[r]

@@ -318,6 +318,14 @@ class OracleSequence:
     def length(self) -> int:
         return self.caches[0].length
 
+    def load_cache(self, layer: int, keys, values) -> None:
+        """Appends positions [length, length + n) of one layer's cache from [n, kv_heads,
+        head_dim] arrays (a cache state produced elsewhere, e.g. read back from the GPU)."""
+        kv = self.caches[layer]
+        k = _f32(keys).reshape(len(keys), -1)
+        v = _f32(values).reshape(len(values), -1)
+        _check(lib().orc_kv_append(C.byref(kv), kv.length, k, v, k.shape[0]), "kv_append")
+
     def cache_arrays(self, layer: int):
         kv = self.caches[layer]
         c_n = kv.length * kv.heads * kv.head_dimension
@@ -373,6 +381,16 @@ class OracleStage:
         lib().orc_final_logits(h, 1, c.hidden_size, _f32(self.w.tensors["model.norm.weight"]),
                                self.w.head, self.w.vocabulary_size, c.rms_norm_epsilon, out)
         return out[0]
+
+    def logits_rows(self, hidden) -> np.ndarray:
+        """final_logits for every row of [rows, hidden] (the per-row final norm + LM head of
+        a decode batch, cpp/src/cuda/stage.cpp:415-436)."""
+        c = self.w.config
+        h = _f32(hidden).reshape(-1, c.hidden_size)
+        out = np.empty((h.shape[0], self.w.vocabulary_size), np.float32)
+        lib().orc_final_logits(h, h.shape[0], c.hidden_size, _f32(self.w.tensors["model.norm.weight"]),
+                               self.w.head, self.w.vocabulary_size, c.rms_norm_epsilon, out)
+        return out
 
     def execute(self, stage_input, position: int, seq: OracleSequence, trace: list | None = None):
         """Returns ('token', id, logprob, top) | ('boundary', f16 bits [T,H]) | ('progress',)."""

@@ -105,8 +105,18 @@ void orc_f16_encode(const float* values, size_t count, uint16_t* out) {
   for (size_t i = 0; i < count; ++i) out[i] = orc_f16_from_f32(values[i]);
 }
 
+static void parallel_elements(size_t count, void (*body)(void*, size_t, size_t), void* context);
+
+static void f16_decode_range(void* context, size_t begin, size_t end) {
+  const void* const* io = (const void* const*)context;
+  const uint16_t* bits = (const uint16_t*)io[0];
+  float* out = (float*)io[1];
+  for (size_t i = begin; i < end; ++i) out[i] = orc_f32_from_f16(bits[i]);
+}
+
 void orc_f16_decode(const uint16_t* bits, size_t count, float* out) {
-  for (size_t i = 0; i < count; ++i) out[i] = orc_f32_from_f16(bits[i]);
+  const void* io[2] = {bits, out};
+  parallel_elements(count, f16_decode_range, (void*)io);
 }
 
 /* ------------------------------------------------------------ layer arithmetic */
@@ -119,6 +129,40 @@ static int thread_count(void) {
   if (g_threads > 0) return g_threads;
   long cores = sysconf(_SC_NPROCESSORS_ONLN);
   return cores > 0 ? (int)(cores > 16 ? 16 : cores) : 1;
+}
+
+typedef struct {
+  void (*body)(void*, size_t, size_t);
+  void* context;
+  size_t begin, end;
+} element_job;
+
+static void* element_worker(void* arg) {
+  element_job* j = (element_job*)arg;
+  j->body(j->context, j->begin, j->end);
+  return NULL;
+}
+
+/* body(context, begin, end) over [0, count) in contiguous ranges, one per thread; element
+ * results do not depend on the split. */
+static void parallel_elements(size_t count, void (*body)(void*, size_t, size_t), void* context) {
+  int threads = thread_count();
+  if (count < (1u << 16)) threads = 1;
+  if (threads > 64) threads = 64;
+  if (threads <= 1) {
+    body(context, 0, count);
+    return;
+  }
+  element_job jobs[64];
+  pthread_t ids[64];
+  const size_t per = (count + (size_t)threads - 1) / (size_t)threads;
+  for (int t = 0; t < threads; ++t) {
+    const size_t b = (size_t)t * per;
+    jobs[t] = (element_job){body, context, b < count ? b : count, b + per < count ? b + per : count};
+  }
+  for (int t = 1; t < threads; ++t) pthread_create(&ids[t], NULL, element_worker, &jobs[t]);
+  element_worker(&jobs[0]);
+  for (int t = 1; t < threads; ++t) pthread_join(ids[t], NULL);
 }
 
 /* cpp/src/cpu/llama.cpp:193-212: y = (x * inv_rms) * w, sequential F32 square sum. */
@@ -589,18 +633,39 @@ static float irwin_hall_normal(uint64_t seed, uint64_t tensor_id, uint64_t index
   return (float)(sum + 6 - 6 * 65536) / 65536.0f;
 }
 
+/* Each element depends only on (seed, tensor, index): ranges are generated in parallel. */
+typedef struct {
+  uint64_t seed, tensor_id, first;
+  float mean, sigma;
+  void* out;
+} synth_job;
+
+static void synth_f32_range(void* context, size_t begin, size_t end) {
+  const synth_job* j = (const synth_job*)context;
+  float* out = (float*)j->out;
+  for (size_t i = begin; i < end; ++i) {
+    const float scaled = irwin_hall_normal(j->seed, j->tensor_id, j->first + i) * j->sigma;
+    out[i] = j->mean + scaled;
+  }
+}
+
+static void synth_f16_range(void* context, size_t begin, size_t end) {
+  const synth_job* j = (const synth_job*)context;
+  uint16_t* out = (uint16_t*)j->out;
+  for (size_t i = begin; i < end; ++i) {
+    const float scaled = irwin_hall_normal(j->seed, j->tensor_id, j->first + i) * j->sigma;
+    out[i] = orc_f16_from_f32(j->mean + scaled);
+  }
+}
+
 void orc_synth_f32(uint64_t seed, uint64_t tensor_id, uint64_t first, size_t count,
                    float mean, float sigma, float* out) {
-  for (size_t i = 0; i < count; ++i) {
-    const float scaled = irwin_hall_normal(seed, tensor_id, first + i) * sigma;
-    out[i] = mean + scaled;
-  }
+  synth_job j = {seed, tensor_id, first, mean, sigma, out};
+  parallel_elements(count, synth_f32_range, &j);
 }
 
 void orc_synth_f16(uint64_t seed, uint64_t tensor_id, uint64_t first, size_t count,
                    float mean, float sigma, uint16_t* out) {
-  for (size_t i = 0; i < count; ++i) {
-    const float scaled = irwin_hall_normal(seed, tensor_id, first + i) * sigma;
-    out[i] = orc_f16_from_f32(mean + scaled);
-  }
+  synth_job j = {seed, tensor_id, first, mean, sigma, out};
+  parallel_elements(count, synth_f16_range, &j);
 }

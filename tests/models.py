@@ -69,3 +69,8 @@ def tiny_rows(tensor, start, count):
     """Rows [start, start+count) of a [1, seq, width] fixture tensor."""
     a = np.asarray(tensor["values"], np.float32).reshape(tensor["shape"])
     return a[0, start:start + count]
+
+
+def f16_normal(rng, shape):
+    """F16 bits of N(0, 1) draws (boundary activations fed to a non-first stage)."""
+    return oracle.f16_encode(rng.standard_normal(shape).astype(np.float32))

@@ -39,7 +39,8 @@ def test_abi_version():
 @pytest.mark.parametrize("struct,cname", [(capi.StageConfig, "hllm_rocm_stage_config"),
                                           (capi.Item, "hllm_rocm_item"),
                                           (capi.Pass, "hllm_rocm_pass"),
-                                          (capi.Memory, "hllm_rocm_memory")])
+                                          (capi.Memory, "hllm_rocm_memory"),
+                                          (capi.PhaseTime, "hllm_rocm_phase_time")])
 def test_struct_layouts_match_header(struct, cname):
     fields = [f for f, _ in struct._fields_]
     body = "\n".join(f'  printf("%zu ", offsetof({cname}, {f}));' for f in fields)

@@ -1,7 +1,9 @@
 """The benchmark's continuous-batching engine against a stand-in stage (no GPU): with the next
 pass planned while the current one runs, every pass still starts each sequence at its current
 length, at most one pass is in flight, no sequence is released or reused while a pass that
-reads it is in flight, and a drained timed region holds exactly the passes it counts."""
+reads it is in flight, a device-fed row only follows a pass that sampled its sequence, and a
+drained timed region holds exactly the passes it counts. The pre-start brings the engine to
+its stated concurrency before the first timed step."""
 import numpy as np
 
 import bench
@@ -22,7 +24,10 @@ class _Lib:
             assert st.live.get(it.sequence), "pass over a released sequence"
             assert it.first_position == st.length[it.sequence]
             assert it.query_tokens >= 1 and it.sequence not in used
+            if it.flags & capi.ITEM_TOKEN_FROM_DEVICE:
+                assert it.query_tokens == 1 and st.sampled.get(it.sequence), "no device token"
             st.length[it.sequence] += it.query_tokens
+            st.sampled[it.sequence] = bool(it.flags & capi.ITEM_SAMPLE)
             used.add(it.sequence)
         st.in_flight = used
         st.passes += 1
@@ -34,12 +39,27 @@ class _Lib:
         return 0
 
 
+class _Ref:
+    def __init__(self, obj):
+        self._obj = obj
+
+
 class _Stage:
     handle = None
 
     def __init__(self):
         self.count, self.length, self.live, self.in_flight, self.passes = 0, {}, {}, None, 0
+        self.sampled = {}
         self.lib = _Lib(self)
+
+    def execute(self, items, token_ids=None):
+        p = capi.Pass()
+        arr = (capi.Item * len(items))(*items)
+        p.items, p.item = len(items), arr
+        assert sum(it.query_tokens for it in items) == len(token_ids)
+        self.lib.hllm_rocm_stage_submit(None, _Ref(p))
+        self.lib.hllm_rocm_stage_wait(None)
+        return {}
 
     def allocate(self, tokens):
         self.count += 1
@@ -66,5 +86,19 @@ def test_pipelined_engine_keeps_sequence_state(monkeypatch):
         tokens += engine.step(last=i == 199)[0]
     assert stage.in_flight is None and stage.passes - before == 200
     assert tokens > 0
+    engine.release_all()
+    assert not any(stage.live.values())
+
+
+def test_prestart_reaches_the_stated_concurrency(monkeypatch):
+    """With no warmup at all, every timed pass holds (nearly) the stated number of requests."""
+    monkeypatch.setattr(capi, "check", lambda status: None)
+    stage = _Stage()
+    engine = bench.Engine(stage, 16, 64, bench.request_stream(np.random.default_rng(4), 1000, 1.0))
+    engine.prestart(np.random.default_rng(5), 1000, 128)
+    assert len(engine.active) == 16 and stage.in_flight is None
+    assert all(stage.sampled[r.seq] for r in engine.active)
+    active = [engine.step(last=i == 99)[3] for i in range(100)]
+    assert min(active) >= 15 and np.mean(active) >= 0.95 * 16
     engine.release_all()
     assert not any(stage.live.values())

@@ -1,0 +1,115 @@
+"""Greedy decoding over at least 64 steps against the CPU oracle (the reference CPU worker's
+arithmetic in F32), through the C ABI, on the two smallest workloads at full depth:
+
+* tiny Llama (2 layers, hidden 64, 4/2 heads, head_dim 16, SwiGLU 128, vocabulary 256,
+  F32 weights ~N(0, 0.02) from seed 0): a prompt of 8 uniform IDs, 64 greedy steps, the
+  oracle run in the test;
+* Qwen3-0.6B (28 layers, vocabulary 151936, F16 weights from seed 0, RMSNorm weights 1.0):
+  8 ragged prompts with lengths uniform in [32, 512] prefilled together in one pass, then
+  128 greedy steps decoded together, against tests/golden/qwen3_0_6b_greedy.json (the
+  oracle's tokens and top-8 logits per step, written by make_greedy_fixture.py).
+
+The GPU feeds back its own tokens (on the device). F32 execution must give the oracle's
+tokens at every step. F16 execution must too, except at a near tie: a step may give a
+different token only if the oracle ranks it within 4e-2 (twice the F16 logit bound) of its
+best, and each departure is reported with the oracle's top-two margin, as the reference's
+checkpoint probe does (tests/cpp/checkpoint_probe.cpp:113-121). After a departure the
+sequence is fed the oracle's tokens from the host, so every later step is still compared.
+At every step the GPU's logits of the oracle's top tokens are within 2e-2 of the oracle's,
+and at least 97% of all steps (and of every sequence's steps) are identical."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from hllm_amd import capi, model, synthetic
+from tests import helpers_parity as hp
+from tests import models
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "qwen3_0_6b_greedy.json")
+LOGIT_TOL, NEAR_TIE, MIN_IDENTICAL = 2e-2, 4e-2, 0.97
+
+
+def _tiny_reference(steps=64):
+    shape = synthetic.TINY_LLAMA
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, shape.vocab, 8).tolist()
+    ost = oracle.OracleStage(models.synthetic_stage(shape, seed=0, norm_sigma=0.0))
+    tokens, logits = ost.generate(prompt, steps)
+    case = {"prompt": prompt, "tokens": tokens, "top_ids": [], "top_logits": []}
+    for lg in logits:
+        order = np.lexsort((np.arange(lg.size), -np.asarray(lg, np.float64)))[:8]
+        case["top_ids"].append([int(i) for i in order])
+        case["top_logits"].append([float(lg[i]) for i in order])
+    return shape, [case], steps
+
+
+def _qwen3_reference():
+    with open(GOLDEN) as f:
+        fx = json.load(f)
+    return synthetic.QWEN3_0_6B, fx["cases"], fx["steps"]
+
+
+def _greedy(shape, cases, steps, execution):
+    """Runs every case's prompt and `steps` greedy steps on the GPU; returns the departures
+    (case, step, oracle token, GPU token, oracle margin) and the identical-step counts."""
+    total = sum(len(c["prompt"]) for c in cases)
+    cfg = model.stage_config(shape, execution=execution, kv_cache_bytes=512 << 20,
+                             max_sequences=len(cases) + 2, max_pass_rows=max(64, total),
+                             max_seq=max(len(c["prompt"]) for c in cases) + steps + 8)
+    st = capi.Stage(cfg)
+    model.synthesize(st, shape, seed=0, norm_sigma=0.0)
+    seqs = [st.allocate(len(c["prompt"]) + steps + 2) for c in cases]
+    forced = [False] * len(cases)
+    departures, identical = [], [0] * len(cases)
+    worst = 0.0
+    for step in range(steps + 1):
+        if step == 0:
+            items = [capi.item(s, len(c["prompt"]), 0) for s, c in zip(seqs, cases)]
+            ids = np.concatenate([np.asarray(c["prompt"], np.uint64) for c in cases])
+        else:
+            items, ids = [], []
+            for i, (s, c) in enumerate(zip(seqs, cases)):
+                pos = len(c["prompt"]) + step - 1
+                items.append(capi.item(s, 1, pos, from_device=not forced[i]))
+                ids.append(c["tokens"][step - 1] if forced[i] else 0)
+        out = st.execute(items, token_ids=ids, want_logits=True)
+        for i, c in enumerate(cases):
+            top_ids, top_vals = c["top_ids"][step], np.asarray(c["top_logits"][step])
+            err = float(np.abs(out["logits"][i][top_ids] - top_vals).max())
+            worst = max(worst, err)
+            assert err <= LOGIT_TOL, (execution, i, step, err)
+            expect, got = int(c["tokens"][step]), int(out["tokens"][i])
+            if got == expect:
+                identical[i] += 1
+                continue
+            margin = float(top_vals[0] - top_vals[1])
+            assert execution == "f16", ("F32 execution departed", i, step, expect, got, margin)
+            assert got in top_ids, ("departure outside the oracle's top tokens", i, step)
+            gap = float(top_vals[0] - top_vals[top_ids.index(got)])
+            assert gap <= NEAR_TIE, ("departure at a clear margin", i, step, gap)
+            departures.append((i, step, expect, got, margin))
+            forced[i] = True
+    st.close()
+    hp.say(f"{shape.name} {execution}: {sum(identical)}/{len(cases) * (steps + 1)} steps identical; "
+           f"largest top-8 logit error {worst:.2e}; departures (case, step, oracle, gpu, oracle "
+           f"top-2 margin): {departures}")
+    return departures, identical
+
+
+@pytest.mark.parametrize("execution", ["f32", "f16"])
+@pytest.mark.parametrize("workload", ["tiny-llama", "qwen3-0.6b"])
+def test_greedy_tokens_identical_for_64_steps(workload, execution):
+    hp.say("greedy identity", workload, execution)
+    shape, cases, steps = _tiny_reference() if workload == "tiny-llama" else _qwen3_reference()
+    assert steps >= 64
+    departures, identical = _greedy(shape, cases, steps, execution)
+    for count in identical:
+        assert count >= MIN_IDENTICAL * (steps + 1), (identical, departures)
+    if execution == "f32":
+        assert not departures
+
