@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBRARY = os.path.join(HERE, "libhllm_rocm.so")
-SOURCES = ["kernels_misc.hip", "gemm.hip", "attention.hip", "sampling.hip", "stage.hip"]
+SOURCES = ["kernels_misc.hip", "gemm.hip", "attention.hip", "sampling.hip", "sample_static.hip", "stage.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          # Packed FP32 instructions stay disabled in device code.

@@ -30,7 +30,9 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_sequence_read_kv", "hllm_rocm_stage_read_tensor", "hllm_rocm_stage_profile", "hllm_rocm_stage_profile_read",
            "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
            "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config",
-           "hllm_rocm_measure_read_bandwidth", "hllm_rocm_stage_execute_profiled")
+           "hllm_rocm_measure_read_bandwidth", "hllm_rocm_stage_execute_profiled",
+           "hllm_rocm_sample_logits_noalloc")
+NOALLOC_MAX_VOCABULARY = 262144
 
 
 class StageError(RuntimeError):
@@ -132,6 +134,7 @@ def library() -> C.CDLL:
     L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
+    L.hllm_rocm_sample_logits_noalloc.argtypes = L.hllm_rocm_sample_logits.argtypes
     for name in EXPORTS:
         fn = getattr(L, name)
         if fn.restype is C.c_int or (fn.restype is None and name != "hllm_rocm_stage_destroy"):
@@ -376,6 +379,26 @@ def sample_logits(logits, options, device: int = 0):
     check(library().hllm_rocm_sample_logits(device, _ptr(lg, C.c_float), rows, vocab, opts,
                                              _ptr(tokens, C.c_uint64), _ptr(logprobs, C.c_double),
                                              _ptr(top_ids, C.c_uint64), _ptr(top_lp, C.c_double)))
+    return tokens, logprobs, top_ids, top_lp
+
+
+def sample_logits_noalloc(logits, options, device: int = 0):
+    """sample_logits through the entry point that allocates nothing (a fixed device area in
+    the library; vocabularies up to NOALLOC_MAX_VOCABULARY)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    if lg.ndim != 2 or len(options) != lg.shape[0]:
+        raise ValueError("one option per row of [rows, vocabulary] logits")
+    rows, vocab = lg.shape
+    opts = (Item * rows)(*options)
+    tokens = np.zeros(rows, np.uint64)
+    logprobs = np.full(rows, np.nan)
+    top_ids = np.full((rows, 5), np.iinfo(np.uint64).max, np.uint64)
+    top_lp = np.full((rows, 5), np.nan)
+    check(library().hllm_rocm_sample_logits_noalloc(device, _ptr(lg, C.c_float), rows, vocab, opts,
+                                                     _ptr(tokens, C.c_uint64),
+                                                     _ptr(logprobs, C.c_double),
+                                                     _ptr(top_ids, C.c_uint64),
+                                                     _ptr(top_lp, C.c_double)))
     return tokens, logprobs, top_ids, top_lp
 
 

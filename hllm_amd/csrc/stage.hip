@@ -133,6 +133,9 @@ constexpr uint64_t kStagingBytes = 64ull << 20;
 }  // namespace
 
 void check_sampling(const hllm_rocm_item& it);
+void sample_logits_noalloc(int32_t device, const float* logits, uint64_t rows, uint64_t V,
+                           const hllm_rocm_item* options, uint64_t* tokens, double* logprobs,
+                           uint64_t* top_ids, double* top_logprobs);
 
 class Stage {
  public:
@@ -1769,6 +1772,15 @@ hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_
                                     uint64_t* top_ids, double* top_logprobs) {
   return guarded([&] {
     hllm_rocm::sample_logits(device, logits, rows, vocabulary, options, tokens, logprobs, top_ids, top_logprobs);
+  });
+}
+
+hllm_status hllm_rocm_sample_logits_noalloc(int32_t device, const float* logits, uint64_t rows, uint64_t vocabulary,
+                                            const hllm_rocm_item* options, uint64_t* tokens, double* logprobs,
+                                            uint64_t* top_ids, double* top_logprobs) {
+  return guarded([&] {
+    hllm_rocm::sample_logits_noalloc(device, logits, rows, vocabulary, options, tokens, logprobs, top_ids,
+                                     top_logprobs);
   });
 }
 

@@ -211,6 +211,23 @@ hllm_status hllm_rocm_sample_logits(int32_t device, const float* logits, uint64_
                                     uint64_t* tokens, double* logprobs, uint64_t* top_ids,
                                     double* top_logprobs);
 
+/* No counterpart in the reference: hllm_rocm_sample_logits for callers that cannot allocate
+ * device memory (serving loops and harnesses that must not call hipMalloc). Same arguments,
+ * results and errors; it allocates nothing (no device or host heap memory, no streams or
+ * events): the rows are staged and sampled two at a time through one fixed area of device
+ * memory in the library, HLLM_ROCM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call
+ * on that GPU until the process ends. Vocabularies above HLLM_ROCM_NOALLOC_MAX_VOCABULARY
+ * are HLLM_RESOURCE_EXHAUSTED. Work runs on the device's null stream and the call returns
+ * when it is done. Calls on one GPU share the area: the library runs one call at a time per
+ * process (a lock), and each call clears what must start at zero; a caller that drives the
+ * area's device from elsewhere while a call runs (another process aside) races with it. */
+#define HLLM_ROCM_NOALLOC_MAX_VOCABULARY 262144u
+#define HLLM_ROCM_NOALLOC_SCRATCH_BYTES 17320704u
+hllm_status hllm_rocm_sample_logits_noalloc(int32_t device, const float* logits, uint64_t rows,
+                                            uint64_t vocabulary, const hllm_rocm_item* options,
+                                            uint64_t* tokens, double* logprobs, uint64_t* top_ids,
+                                            double* top_logprobs);
+
 /* Replay of repeated pass shapes (items, rows, sampled rows, sampler use, attention work
  * items) from captured HIP graphs, off by default: a shape's second pass is captured and
  * later ones replay it, with the same kernels and results as eager launches and less host
