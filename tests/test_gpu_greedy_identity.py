@@ -58,7 +58,7 @@ def _greedy(shape, cases, steps, execution):
     """Runs every case's prompt and `steps` greedy steps on the GPU; returns the departures
     (case, step, oracle token, GPU token, oracle margin) and the identical-step counts."""
     total = sum(len(c["prompt"]) for c in cases)
-    cfg = model.stage_config(shape, execution=execution, kv_cache_bytes=512 << 20,
+    cfg = model.stage_config(shape, execution=execution, kv_cache_bytes=2 << 30,
                              max_sequences=len(cases) + 2, max_pass_rows=max(64, total),
                              max_seq=max(len(c["prompt"]) for c in cases) + steps + 8)
     st = capi.Stage(cfg)
