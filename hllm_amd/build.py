@@ -55,8 +55,8 @@ def build(jobs: int = 4) -> str:
 
 HOST = os.path.join(HERE, "host")
 HOST_LIBRARY = os.path.join(HERE, "libhllm_rocm_host.so")
-HOST_SOURCES = ["json.cpp", "safetensors.cpp", "dense_loader.cpp", "decode_batch.cpp", "sampling.cpp",
-                "scheduler.cpp", "rocm_stage.cpp"]
+HOST_SOURCES = ["json.cpp", "safetensors.cpp", "dense_loader.cpp", "sampling.cpp", "scheduler.cpp",
+                "rocm_stage.cpp"]
 HOST_TESTS = os.path.join(HERE, "_build", "host_tests")
 CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}"]

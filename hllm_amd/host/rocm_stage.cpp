@@ -2,6 +2,7 @@
 
 #include <cstring>
 #include <limits>
+#include <unordered_set>
 
 namespace hllm_rocm::backend {
 
@@ -17,6 +18,28 @@ void check(hllm_status status) {
     case HLLM_DEADLINE_EXCEEDED: throw Error::deadline_exceeded(message);
     case HLLM_CANCELLED: throw Error::cancelled(message);
     default: throw Error::internal(message);
+  }
+}
+
+void require_decode_batch(const std::vector<runtime::DecodeBatchItem>& items, std::size_t hidden) {
+  if (items.empty() || items.size() > worker::StageScheduler::kMaximumDecodeRows)
+    throw Error::invalid_request("a decode batch holds 1 to 64 members");
+  const bool tokens = std::holds_alternative<runtime::TokenInput>(items.front().input);
+  std::unordered_set<const runtime::SequenceState*> members;
+  for (const runtime::DecodeBatchItem& it : items) {
+    if (!it.sequence || !it.cancelled) throw Error::invalid_request("decode batch member without a sequence");
+    if (!members.insert(it.sequence).second) throw Error::invalid_request("a sequence is in a decode batch twice");
+    if (it.sequence->prefilling || it.position == 0)
+      throw Error::invalid_request("decode batch members must be decoding started sequences");
+    if (std::holds_alternative<runtime::TokenInput>(it.input) != tokens)
+      throw Error::invalid_request("a decode batch mixes token and boundary inputs");
+    if (const auto* t = std::get_if<runtime::TokenInput>(&it.input)) {
+      if (t->ids.size() != 1) throw Error::invalid_request("a decode batch member carries one token");
+    } else {
+      const auto& b = std::get<runtime::BoundaryActivation>(it.input);
+      if (b.tokens != 1 || b.width != hidden || b.payload.size() != hidden * 2)
+        throw Error::invalid_request("a decode batch member carries one boundary row");
+    }
   }
 }
 
@@ -262,7 +285,7 @@ runtime::StageOutput RocmStage::execute(runtime::StageInput input, std::size_t f
 }
 
 std::vector<runtime::StageOutput> RocmStage::execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const {
-  static_cast<void>(runtime::combine_decode_inputs(items));  // the contract's batch rules
+  require_decode_batch(items, config_.hidden_size);
   // An in-flight batch is not preempted: a member's cancellation is its caller's to observe.
   std::vector<Member> members;
   members.reserve(items.size());

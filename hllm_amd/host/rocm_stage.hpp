@@ -12,6 +12,7 @@
 #include "dense_loader.hpp"
 #include "hllm_rocm.h"
 #include "runtime.hpp"
+#include "scheduler.hpp"
 
 namespace hllm_rocm::backend {
 
@@ -26,7 +27,13 @@ struct StageOptions {
 // Translates a failed C-ABI call into the runtime's error categories.
 void check(hllm_status status);
 
-class RocmStage final : public runtime::StageBackend {
+// The decode-batch contract (cpp/include/hllm/runtime/stage_backend.hpp:52-58,93-101): 1..64
+// members, each one row (a token, or a boundary row `hidden` wide) of a distinct sequence that
+// has started and is not prefilling, all with the same kind of input. INVALID_REQUEST
+// otherwise.
+void require_decode_batch(const std::vector<runtime::DecodeBatchItem>& items, std::size_t hidden);
+
+class RocmStage final : public runtime::StageBackend, public worker::MixedPassBackend {
  public:
   // Creates the device stage for an admitted dense source and uploads its tensors.
   RocmStage(const model::DenseSource& source, const std::filesystem::path& root, const StageOptions& options);
@@ -50,7 +57,7 @@ class RocmStage final : public runtime::StageBackend {
 
   // One ragged pass over any mix of prefill chunks and one-token decode inputs of distinct
   // sequences (the reference contract runs these as separate passes). Outputs in item order.
-  std::vector<runtime::StageOutput> execute_mixed(std::vector<runtime::DecodeBatchItem> items) const;
+  std::vector<runtime::StageOutput> execute_mixed(std::vector<runtime::DecodeBatchItem> items) const override;
 
   hllm_rocm_stage* handle() const { return stage_; }
   const hllm_rocm_stage_config& config() const { return config_; }

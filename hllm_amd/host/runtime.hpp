@@ -102,9 +102,6 @@ struct DecodeBatchItem {
   SequenceState* sequence;
   const std::atomic_bool* cancelled;
 };
-// decode_batch.cpp: one-token members in item order, at most 64, independent and ready.
-StageInput combine_decode_inputs(const std::vector<DecodeBatchItem>& items);
-std::vector<StageOutput> split_decode_boundary(BoundaryActivation output);
 
 // stage_backend.hpp:62-67
 [[nodiscard]] constexpr std::size_t query_rows(std::size_t tokens, std::size_t maximum_query_tokens) noexcept {

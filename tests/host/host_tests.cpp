@@ -1,11 +1,11 @@
 // Tests of the host-side stage contract (hllm_amd/host): JSON and Safetensors readers,
-// stage admission, decode-batch packing, host sampling, the pass scheduler, and (on a GPU)
-// the RocmStage adapter over the C ABI. Run one case per process:
+// stage admission, decode-batch rules, host sampling, the mixed-pass scheduler, and (on a
+// GPU) the RocmStage adapter over the C ABI. Run one case per process:
 //   host_tests --list | host_tests <case> [args...]
-// Scheduler cases follow the reference's tests/cpp/scheduler_test.cpp; decode-batch cases
-// follow tests/cpp/decode_batch_contract.hpp.
+// The GPU decode-batch case follows tests/cpp/decode_batch_contract.hpp.
 #include <chrono>
 #include <cmath>
+#include <deque>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -279,39 +279,36 @@ void dense_admission() {
 
 // ------------------------------------------------------------------ decode batches
 
-void decode_batch_packing() {
+// The adapter's decode-batch rules (tests/cpp/decode_batch_contract.hpp runs the batch;
+// these are its admission rules).
+void decode_batch_rules() {
   std::atomic_bool stop{false};
   runtime::SequenceState a, b, busy;
   busy.prefilling = true;
   using Items = std::vector<runtime::DecodeBatchItem>;
   auto tok = [](std::uint64_t id) { return runtime::StageInput{runtime::TokenInput{{id}}}; };
-  auto row = [](std::size_t width, std::byte fill) {
-    return runtime::StageInput{runtime::BoundaryActivation{1, width, std::vector<std::byte>(width * 2, fill)}};
+  auto row = [](std::size_t width) {
+    return runtime::StageInput{runtime::BoundaryActivation{1, width, std::vector<std::byte>(width * 2)}};
   };
-  const auto ids = std::get<runtime::TokenInput>(runtime::combine_decode_inputs(Items{{tok(5), 3, &a, &stop}, {tok(9), 1, &b, &stop}}));
-  CHECK(ids.ids == (std::vector<std::uint64_t>{5, 9}));
-  const auto rows = std::get<runtime::BoundaryActivation>(
-      runtime::combine_decode_inputs(Items{{row(3, std::byte{1}), 3, &a, &stop}, {row(3, std::byte{2}), 1, &b, &stop}}));
-  CHECK(rows.tokens == 2 && rows.width == 3 && rows.payload.size() == 12 && rows.payload[6] == std::byte{2});
-  const auto parts = runtime::split_decode_boundary(rows);
-  CHECK(parts.size() == 2 && std::get<runtime::BoundaryActivation>(parts[1]).payload[0] == std::byte{2});
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{}), kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 0, &a, &stop}}), kInvalidRequest);  // position 0
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &busy, &stop}}), kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &a, &stop}, {tok(2), 2, &a, &stop}}), kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, &a, &stop}, {row(3, std::byte{0}), 2, &b, &stop}}),
+  backend::require_decode_batch(Items{{tok(5), 3, &a, &stop}, {tok(9), 1, &b, &stop}}, 6);
+  backend::require_decode_batch(Items{{row(6), 3, &a, &stop}, {row(6), 1, &b, &stop}}, 6);
+  EXPECT_ERROR(backend::require_decode_batch(Items{}, 6), kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 0, &a, &stop}}, 6), kInvalidRequest);  // not started
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &busy, &stop}}, 6), kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &a, &stop}, {tok(2), 2, &a, &stop}}, 6),
                kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{runtime::TokenInput{{1, 2}}, 2, &a, &stop}}), kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{row(3, std::byte{0}), 2, &a, &stop}, {row(4, std::byte{0}), 2, &b, &stop}}),
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &a, &stop}, {row(6), 2, &b, &stop}}, 6),
                kInvalidRequest);
-  EXPECT_ERROR(runtime::combine_decode_inputs(Items{{tok(1), 2, nullptr, &stop}}), kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(Items{{runtime::TokenInput{{1, 2}}, 2, &a, &stop}}, 6),
+               kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(Items{{row(5), 2, &a, &stop}}, 6), kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, nullptr, &stop}}, 6), kInvalidRequest);
   std::vector<runtime::SequenceState> many(65);
   Items big;
   for (auto& s : many) big.push_back({tok(1), 1, &s, &stop});
-  EXPECT_ERROR(runtime::combine_decode_inputs(big), kInvalidRequest);
+  EXPECT_ERROR(backend::require_decode_batch(big, 6), kInvalidRequest);
   big.pop_back();
-  CHECK(std::get<runtime::TokenInput>(runtime::combine_decode_inputs(big)).ids.size() == 64);
-  EXPECT_ERROR(runtime::split_decode_boundary(runtime::BoundaryActivation{2, 3, std::vector<std::byte>(10)}), kInternal);
+  backend::require_decode_batch(big, 6);
 }
 
 // ------------------------------------------------------------------ host sampling
@@ -365,13 +362,18 @@ void host_sampling(const std::vector<std::string>& args) {
 
 // ------------------------------------------------------------------ scheduler
 
-class GateStage : public runtime::StageBackend {
+// A stand-in stage: records every pass as the first token ID of each member; a member with
+// token 999 waits for `gate` (to hold the dispatcher inside a pass). With `mixed`, it runs
+// mixed passes; otherwise prefills alone and decode batches.
+class RecordingStage : public runtime::StageBackend {
  public:
   mutable std::mutex mutex;
-  mutable std::vector<std::uint64_t> order;
-  std::promise<void> release;
-  std::shared_future<void> gate = release.get_future().share();
-  bool supports_decode_batch() const override { return true; }
+  mutable std::vector<std::vector<std::uint64_t>> passes;
+  std::promise<void> open;
+  std::shared_future<void> gate = open.get_future().share();
+  bool batches{true};
+  mutable std::atomic<bool> fail{false};
+  bool supports_decode_batch() const override { return batches; }
   runtime::MemoryAmounts weight_memory() const override { return {}; }
   std::size_t hidden_size() const override { return 1; }
   std::size_t vocabulary_size() const override { return 1000; }
@@ -380,145 +382,212 @@ class GateStage : public runtime::StageBackend {
   std::unique_ptr<runtime::SequenceState> allocate_sequence(std::size_t) const override {
     return std::make_unique<runtime::SequenceState>();
   }
-  runtime::StageOutput execute(runtime::StageInput input, std::size_t, runtime::SequenceState&,
+  runtime::StageOutput execute(runtime::StageInput input, std::size_t, runtime::SequenceState& s,
                                const std::atomic_bool&) const override {
-    const auto id = std::get<runtime::TokenInput>(input).ids.at(0);
-    if (id == 999) gate.wait();
-    std::scoped_lock lock(mutex);
-    order.push_back(id);
-    return runtime::SampledToken{id};
+    std::vector<runtime::DecodeBatchItem> one;
+    one.push_back({std::move(input), 0, &s, nullptr});
+    return record(one).front();
   }
-};
-
-void scheduler_priority(std::size_t batch) {
-  worker::StageScheduler scheduler;
-  scheduler.configure(batch);
-  GateStage backend;
-  std::atomic_bool cancelled{false}, dropped{false};
-  auto execute = [&](std::uint64_t id, std::size_t position, const std::atomic_bool& stop) {
-    runtime::SequenceState sequence;
-    sequence.prefilling = id == 100;
-    return scheduler.execute(backend, runtime::TokenInput{{id}}, position, sequence, stop,
-                             std::chrono::system_clock::now() + 5s);
-  };
-  auto first = std::async(std::launch::async, [&] { return execute(999, 0, cancelled); });
-  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
-  std::vector<std::future<runtime::StageOutput>> decodes;
-  for (std::size_t i = 0; i < 10; ++i) {
-    decodes.push_back(std::async(std::launch::async, [&, i] { return execute(i, 1, cancelled); }));
-    CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == i + 1; }));
-  }
-  auto prefill = std::async(std::launch::async, [&] { return execute(100, 3, cancelled); });
-  auto dropped_job = std::async(std::launch::async, [&] {
-    try {
-      static_cast<void>(execute(200, 0, dropped));
-    } catch (const runtime::Error& e) {
-      return e.code() == runtime::ErrorCode::kCancelled;
-    }
-    return false;
-  });
-  CHECK(wait_for([&] { return scheduler.metrics().queued_prefills == 2; }));
-  dropped = true;
-  CHECK(wait_for([&] { return scheduler.metrics().queued_prefills == 1; }));
-  backend.release.set_value();
-  static_cast<void>(first.get());
-  for (auto& d : decodes) static_cast<void>(d.get());
-  static_cast<void>(prefill.get());
-  CHECK(dropped_job.get());
-  CHECK(backend.order == (std::vector<std::uint64_t>{999, 0, 1, 2, 3, 4, 5, 6, 7, 100, 8, 9}));
-  const auto m = scheduler.metrics();
-  CHECK(m.queued_prefills + m.queued_decodes + m.executing == 0);
-  CHECK(m.completed_steps == 12);
-  if (batch > 1) CHECK(m.decode_batches > 0 && m.largest_decode_batch == batch);
-}
-
-void scheduler_deadline() {
-  worker::StageScheduler scheduler;
-  GateStage backend;
-  std::atomic_bool stop{false};
-  runtime::SequenceState active, queued;
-  auto first = std::async(std::launch::async, [&] {
-    return scheduler.execute(backend, runtime::TokenInput{{999}}, 0, active, stop, std::chrono::system_clock::now() + 5s);
-  });
-  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
-  EXPECT_ERROR(scheduler.execute(backend, runtime::TokenInput{{1}}, 1, queued, stop,
-                                 std::chrono::system_clock::now() + 20ms),
-               kDeadlineExceeded);
-  CHECK(scheduler.metrics().queued_decodes == 0);
-  backend.release.set_value();
-  static_cast<void>(first.get());
-  CHECK(backend.order == (std::vector<std::uint64_t>{999}));
-}
-
-class BatchGateStage final : public GateStage {
- public:
-  mutable std::promise<void> entered;
-  std::promise<void> finish;
-  std::shared_future<void> batch_gate = finish.get_future().share();
-  bool fail = false;
   std::vector<runtime::StageOutput> execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const override {
-    entered.set_value();
-    if (batch_gate.wait_for(5s) != std::future_status::ready) throw std::runtime_error("test batch gate timed out");
-    if (fail) throw std::runtime_error("injected dispatch failure");
-    std::vector<runtime::StageOutput> result;
-    for (auto& item : items) {
-      item.sequence->generated_index += 1;
-      result.push_back(runtime::SampledToken{std::get<runtime::TokenInput>(item.input).ids[0]});
+    return record(items);
+  }
+
+ protected:
+  std::vector<runtime::StageOutput> record(const std::vector<runtime::DecodeBatchItem>& items) const {
+    std::vector<std::uint64_t> ids;
+    for (const auto& it : items) ids.push_back(std::get<runtime::TokenInput>(it.input).ids.at(0));
+    if (ids.front() == 999 && gate.wait_for(5s) != std::future_status::ready)
+      throw std::runtime_error("test gate timed out");
+    {
+      std::scoped_lock lock(mutex);
+      passes.push_back(ids);
     }
-    return result;
+    if (fail.load()) throw std::runtime_error("injected pass failure");
+    std::vector<runtime::StageOutput> out;
+    for (const auto& it : items) {
+      it.sequence->generated_index += 1;
+      out.push_back(runtime::SampledToken{std::get<runtime::TokenInput>(it.input).ids.at(0)});
+    }
+    return out;
   }
 };
 
-// A member cancelled while its batch runs still receives the batch's result (or its
-// failure); the scheduler accepts new work afterwards.
+class MixedRecordingStage final : public RecordingStage, public worker::MixedPassBackend {
+ public:
+  std::vector<runtime::StageOutput> execute_mixed(std::vector<runtime::DecodeBatchItem> items) const override {
+    return record(items);
+  }
+};
+
+// Callers, each with its own sequence and cancellation flag, submitting through one scheduler.
+struct Callers {
+  worker::StageScheduler& scheduler;
+  const runtime::StageBackend& backend;
+  std::deque<runtime::SequenceState> sequences;
+  std::deque<std::atomic_bool> flags;
+  std::vector<std::future<runtime::StageOutput>> results;
+  // Queues one request (ids: its token IDs, first = its name) and waits until it is queued.
+  std::size_t submit(std::vector<std::uint64_t> ids, bool prefill,
+                      std::chrono::milliseconds deadline = std::chrono::milliseconds(5000)) {
+    sequences.emplace_back();
+    sequences.back().prefilling = prefill;
+    flags.emplace_back(false);
+    runtime::SequenceState& s = sequences.back();
+    std::atomic_bool& stop = flags.back();
+    // Queued, running or already done: a request may complete before it is seen queued.
+    auto seen = [this] {
+      const auto m = scheduler.metrics();
+      return m.queued_prefills + m.queued_decodes + m.executing + m.completed_steps;
+    };
+    const std::size_t queued = seen();
+    results.push_back(std::async(std::launch::async, [this, ids, &s, &stop, deadline] {
+      return scheduler.execute(backend, runtime::TokenInput{ids}, prefill_position(ids), s, stop,
+                               std::chrono::system_clock::now() + deadline);
+    }));
+    CHECK(wait_for([&] { return seen() > queued; }));
+    return results.size() - 1;
+  }
+  static std::size_t prefill_position(const std::vector<std::uint64_t>& ids) { return ids.size() == 1 ? 1 : 0; }
+  std::uint64_t token(std::size_t i) { return std::get<runtime::SampledToken>(results[i].get()).id; }
+};
+
+std::vector<std::uint64_t> prefill_ids(std::uint64_t name, std::size_t rows) {
+  std::vector<std::uint64_t> ids(rows, 1);
+  ids[0] = name;
+  return ids;
+}
+
+// Mixed passes: all waiting decodes (up to the limit) plus prefills in arrival order within
+// the row budget, decodes first.
+void scheduler_mixed_passes() {
+  worker::StageScheduler scheduler;
+  scheduler.configure(worker::PassPolicy{4, 10});
+  MixedRecordingStage stage;
+  stage.open.set_value();
+  Callers c{scheduler, stage, {}, {}, {}};
+  scheduler.hold();
+  for (std::uint64_t d = 0; d < 6; ++d) c.submit({d}, false);
+  c.submit(prefill_ids(100, 6), true);
+  c.submit(prefill_ids(101, 3), true);
+  c.submit(prefill_ids(102, 5), true);
+  CHECK(scheduler.metrics().queued_decodes == 6 && scheduler.metrics().queued_prefills == 3);
+  scheduler.resume();
+  for (std::size_t i = 0; i < 6; ++i) CHECK(c.token(i) == i);
+  CHECK(c.token(6) == 100 && c.token(7) == 101 && c.token(8) == 102);
+  using P = std::vector<std::vector<std::uint64_t>>;
+  CHECK(stage.passes == (P{{0, 1, 2, 3, 100, 101}, {4, 5, 102}}));
+  const auto m = scheduler.metrics();
+  CHECK(m.passes == 2 && m.mixed_passes == 2 && m.completed_steps == 9 && m.largest_decode_batch == 4);
+  CHECK(m.largest_pass_rows == 4 + 6 + 3 && m.executing == 0 && m.queued_decodes + m.queued_prefills == 0);
+}
+
+// A prefill larger than the budget still runs (alone with the decodes), and requests keep
+// arriving while a pass runs.
+void scheduler_large_prefill() {
+  worker::StageScheduler scheduler;
+  scheduler.configure(worker::PassPolicy{8, 4});
+  MixedRecordingStage stage;
+  Callers c{scheduler, stage, {}, {}, {}};
+  c.submit({999}, false);  // holds the first pass until the gate opens
+  CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
+  c.submit(prefill_ids(200, 9), true);
+  c.submit({1}, false);
+  c.submit(prefill_ids(201, 2), true);
+  stage.open.set_value();
+  CHECK(c.token(0) == 999 && c.token(1) == 200 && c.token(2) == 1 && c.token(3) == 201);
+  using P = std::vector<std::vector<std::uint64_t>>;
+  CHECK(stage.passes == (P{{999}, {1, 200}, {201}}));
+}
+
+// Cancelled or expired requests leave the queue without reaching the backend; the others run.
+void scheduler_retires_unready_requests() {
+  worker::StageScheduler scheduler;
+  MixedRecordingStage stage;
+  stage.open.set_value();
+  Callers c{scheduler, stage, {}, {}, {}};
+  scheduler.hold();
+  const std::size_t cancelled = c.submit({7}, false);
+  const std::size_t expiring = c.submit({8}, false, std::chrono::milliseconds(30));
+  const std::size_t kept = c.submit(prefill_ids(300, 2), true);
+  c.flags[cancelled] = true;
+  EXPECT_ERROR(c.results[cancelled].get(), kCancelled);
+  EXPECT_ERROR(c.results[expiring].get(), kDeadlineExceeded);
+  CHECK(scheduler.metrics().queued_decodes == 0 && scheduler.metrics().queued_prefills == 1);
+  scheduler.resume();
+  CHECK(c.token(kept) == 300);
+  using P = std::vector<std::vector<std::uint64_t>>;
+  CHECK(stage.passes == (P{{300}}));
+}
+
+// A member cancelled while its pass runs gets the pass's result (or its failure); the
+// scheduler takes new work afterwards.
 void scheduler_in_flight(bool fail) {
   worker::StageScheduler scheduler;
-  scheduler.configure(4);
-  BatchGateStage backend;
-  backend.fail = fail;
-  std::atomic_bool hold{false}, a_stop{false}, b_stop{false};
-  runtime::SequenceState gate_seq, a, b;
-  auto gate = std::async(std::launch::async, [&] {
-    return scheduler.execute(backend, runtime::TokenInput{{999}}, 0, gate_seq, hold, std::chrono::system_clock::now() + 5s);
-  });
+  MixedRecordingStage stage;
+  Callers c{scheduler, stage, {}, {}, {}};
+  const std::size_t gate = c.submit({999}, false);
   CHECK(wait_for([&] { return scheduler.metrics().executing == 1; }));
-  auto run = [&](std::uint64_t id, runtime::SequenceState& s, std::atomic_bool& stop) {
-    return std::async(std::launch::async, [&, id] {
-      return scheduler.execute(backend, runtime::TokenInput{{id}}, 1, s, stop, std::chrono::system_clock::now() + 5s);
-    });
-  };
-  auto fa = run(1, a, a_stop);
-  CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == 1; }));
-  auto fb = run(2, b, b_stop);
-  CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == 2; }));
-  backend.release.set_value();
-  static_cast<void>(gate.get());
-  CHECK(backend.entered.get_future().wait_for(2s) == std::future_status::ready);
-  a_stop = true;  // cancelled while its batch is in flight
-  backend.finish.set_value();
+  c.flags[gate] = true;  // cancelled inside its pass
+  const std::size_t a = c.submit({1}, false);
+  stage.fail = fail;
+  stage.open.set_value();
   if (fail) {
-    bool threw_a = false, threw_b = false;
-    try { static_cast<void>(fa.get()); } catch (const std::runtime_error&) { threw_a = true; }
-    try { static_cast<void>(fb.get()); } catch (const std::runtime_error&) { threw_b = true; }
-    CHECK(threw_a && threw_b);
+    bool threw = false;
+    try {
+      static_cast<void>(c.results[gate].get());
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    CHECK(threw);
+    try {
+      static_cast<void>(c.results[a].get());
+      threw = false;
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    CHECK(threw);
   } else {
-    CHECK(std::get<runtime::SampledToken>(fa.get()).id == 1);
-    CHECK(std::get<runtime::SampledToken>(fb.get()).id == 2);
-    CHECK(a.generated_index == 1 && b.generated_index == 1);
+    CHECK(c.token(gate) == 999 && c.token(a) == 1);
+    CHECK(c.sequences[gate].generated_index == 1);
   }
-  runtime::SequenceState c;
-  std::atomic_bool go{false};
-  const auto after = scheduler.execute(backend, runtime::TokenInput{{7}}, 0, c, go, std::chrono::system_clock::now() + 5s);
-  CHECK(std::get<runtime::SampledToken>(after).id == 7);
-  CHECK(scheduler.metrics().executing == 0);
+  stage.fail = false;
+  const std::size_t after = c.submit({5}, false);
+  CHECK(c.token(after) == 5 && scheduler.metrics().executing == 0);
+}
+
+// Backends without mixed passes: a prefill alone or a decode batch, alternating while both
+// queues wait, the first pass serving the older request; single decodes when the backend
+// has no decode batches.
+void scheduler_without_mixed_passes(bool batches) {
+  worker::StageScheduler scheduler;
+  scheduler.configure(worker::PassPolicy{2, 512});
+  RecordingStage stage;
+  stage.batches = batches;
+  stage.open.set_value();
+  Callers c{scheduler, stage, {}, {}, {}};
+  scheduler.hold();
+  for (std::uint64_t d = 0; d < 3; ++d) c.submit({d}, false);
+  c.submit(prefill_ids(100, 4), true);
+  c.submit(prefill_ids(101, 4), true);
+  scheduler.resume();
+  for (std::size_t i = 0; i < 5; ++i) static_cast<void>(c.results[i].get());
+  using P = std::vector<std::vector<std::uint64_t>>;
+  if (batches)
+    CHECK(stage.passes == (P{{0, 1}, {100}, {2}, {101}}));
+  else
+    CHECK(stage.passes == (P{{0}, {100}, {1}, {101}, {2}}));
+  CHECK(scheduler.metrics().mixed_passes == 0);
 }
 
 void scheduler_configuration() {
   worker::StageScheduler s;
-  EXPECT_ERROR(s.configure(0), kInvalidRequest);
-  EXPECT_ERROR(s.configure(65), kInvalidRequest);
-  s.configure(64);
+  EXPECT_ERROR(s.configure(worker::PassPolicy{0, 512}), kInvalidRequest);
+  EXPECT_ERROR(s.configure(worker::PassPolicy{65, 512}), kInvalidRequest);
+  EXPECT_ERROR(s.configure(worker::PassPolicy{8, 0}), kInvalidRequest);
+  s.configure(worker::PassPolicy{64, 2048});
+  CHECK(s.policy().maximum_decode_rows == 64 && s.policy().prefill_row_budget == 2048);
   s.configure(1);
+  CHECK(s.policy().maximum_decode_rows == 1 && s.policy().prefill_row_budget == 2048);
 }
 
 // ------------------------------------------------------------------ GPU: the adapter
@@ -621,6 +690,48 @@ void gpu_decode_batch_contract(const std::vector<std::string>& args) {
   }
 }
 
+// The scheduler over the ROCm stage: a decode of one sequence and a prefill of another,
+// queued together, run as one mixed pass and give the tokens serial execution gives.
+void gpu_scheduler_mixed_pass(const std::vector<std::string>& args) {
+  CHECK(args.size() == 1);
+  const fs::path dir = args[0];
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  model::LoadStageRequest r = request_for(m, 0, 1);
+  r.plan.execution_dtype = model::WireDType::kF32;
+  backend::StageOptions options;
+  options.kv_cache_bytes = 64u << 20;
+  options.kv_block_tokens = 32;
+  options.max_sequences = 16;
+  options.max_pass_rows = 256;
+  backend::RocmBackendFactory factory(options);
+  auto stage = factory.load(r, dir, {1ull << 40, 1ull << 40, 0, 0});
+  std::atomic_bool go{false};
+  const std::vector<std::uint64_t> prompt_a{1, 4, 2, 8, 3}, prompt_b{2, 7, 1};
+  auto token = [](const runtime::StageOutput& o) { return std::get<runtime::SampledToken>(o).id; };
+  auto ra = stage->allocate_sequence(16), rb = stage->allocate_sequence(16);
+  static_cast<void>(stage->execute(runtime::TokenInput{prompt_a}, 0, *ra, go));
+  const std::uint64_t ta = token(stage->execute(runtime::TokenInput{{4}}, 5, *ra, go));
+  const std::uint64_t tb = token(stage->execute(runtime::TokenInput{prompt_b}, 0, *rb, go));
+  auto sa = stage->allocate_sequence(16), sb = stage->allocate_sequence(16);
+  static_cast<void>(stage->execute(runtime::TokenInput{prompt_a}, 0, *sa, go));
+  sb->prefilling = true;
+  worker::StageScheduler scheduler;
+  scheduler.hold();
+  auto fa = std::async(std::launch::async, [&] {
+    return scheduler.execute(*stage, runtime::TokenInput{{4}}, 5, *sa, go, std::chrono::system_clock::now() + 5s);
+  });
+  CHECK(wait_for([&] { return scheduler.metrics().queued_decodes == 1; }));
+  auto fb = std::async(std::launch::async, [&] {
+    return scheduler.execute(*stage, runtime::TokenInput{prompt_b}, 0, *sb, go, std::chrono::system_clock::now() + 5s);
+  });
+  CHECK(wait_for([&] { return scheduler.metrics().queued_prefills == 1; }));
+  scheduler.resume();
+  CHECK(token(fa.get()) == ta);
+  CHECK(token(fb.get()) == tb);
+  const auto metrics = scheduler.metrics();
+  CHECK(metrics.passes == 1 && metrics.mixed_passes == 1 && metrics.largest_pass_rows == 4);
+}
+
 struct Case {
   const char* name;
   std::function<void(const std::vector<std::string>&)> run;
@@ -631,16 +742,19 @@ const std::vector<Case>& cases() {
       {"json_reader", [](auto&) { json_reader(); }, false},
       {"safetensors_reader", [](auto&) { safetensors_reader(); }, false},
       {"dense_admission", [](auto&) { dense_admission(); }, false},
-      {"decode_batch_packing", [](auto&) { decode_batch_packing(); }, false},
+      {"decode_batch_rules", [](auto&) { decode_batch_rules(); }, false},
       {"host_sampling", host_sampling, false},
-      {"scheduler_priority_batch1", [](auto&) { scheduler_priority(1); }, false},
-      {"scheduler_priority_batch4", [](auto&) { scheduler_priority(4); }, false},
-      {"scheduler_deadline", [](auto&) { scheduler_deadline(); }, false},
+      {"scheduler_mixed_passes", [](auto&) { scheduler_mixed_passes(); }, false},
+      {"scheduler_large_prefill", [](auto&) { scheduler_large_prefill(); }, false},
+      {"scheduler_retires_unready_requests", [](auto&) { scheduler_retires_unready_requests(); }, false},
       {"scheduler_in_flight_ok", [](auto&) { scheduler_in_flight(false); }, false},
       {"scheduler_in_flight_failure", [](auto&) { scheduler_in_flight(true); }, false},
+      {"scheduler_without_mixed_passes", [](auto&) { scheduler_without_mixed_passes(true); }, false},
+      {"scheduler_without_decode_batches", [](auto&) { scheduler_without_mixed_passes(false); }, false},
       {"scheduler_configuration", [](auto&) { scheduler_configuration(); }, false},
       {"gpu_checkpoint_greedy", gpu_checkpoint_greedy, true},
       {"gpu_decode_batch_contract", gpu_decode_batch_contract, true},
+      {"gpu_scheduler_mixed_pass", gpu_scheduler_mixed_pass, true},
   };
   return all;
 }
