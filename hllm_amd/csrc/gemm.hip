@@ -987,6 +987,185 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
 }  // namespace
 
 
+// Decode projections (F16, at most 16 * MF rows): every wave streams the weights of its own
+// NFW fragment rows (16 features each) over the workgroup's K range through a P-deep register
+// ring, so weights are read exactly once and no K-wave reduction is needed. The rows'
+// activations are staged in LDS in double-buffered chunks of KC k-steps, once per workgroup
+// of WAVES waves. With PAIR, a wave's two fragment rows are a gate fragment and its up
+// fragment (rows 4g + h and 4g + 2 + h of the interleaved gate/up matrix), so SwiGLU is
+// applied from the accumulators and no split-K reduction is ever needed for it. K is split
+// across workgroups only for deferred consumers (the K-split partials are summed in split
+// order by the kernel that reads the projection).
+template <int MF, int WAVES, int NFW, int KC, int P, bool PAIR>
+__global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int n_tiles) {
+  constexpr int NT = 64 * WAVES, FR = WAVES * NFW;
+  constexpr int CHUNK = MF * KC * 64;  // half8s per staged chunk
+  constexpr int PIECES = (CHUNK + NT - 1) / NT;
+  static_assert(KC % P == 0, "the ring slot of a k-step must be a compile-time index");
+  static_assert(!PAIR || (NFW == 2 && WAVES % 2 == 0), "gate/up pairs: two fragment rows per wave");
+  extern __shared__ float lds[];
+  half8* xs = reinterpret_cast<half8*>(lds);  // [2][MF][KC][64]
+  const int M = a.device_m ? *a.device_m : a.M;
+  const int tile_n = blockIdx.x % n_tiles, split = blockIdx.x / n_tiles;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int KT = (int)(a.Kp >> 5);
+  const int per = ((KT + a.ksplit - 1) / a.ksplit + KC - 1) / KC * KC;
+  const int kt0 = split * per, kt1 = min(KT, kt0 + per);
+  const int steps = kt1 > kt0 ? kt1 - kt0 : 0;
+  const int chunks = (steps + KC - 1) / KC;
+  const size_t frag_stride = (size_t)KT * 64;
+  // This wave's fragment rows.
+  int frag[NFW];
+  if constexpr (PAIR) {
+    const int group = tile_n * (FR / 4) + (wave >> 1), h = wave & 1;
+    frag[0] = 4 * group + h;
+    frag[1] = 4 * group + 2 + h;
+  } else {
+#pragma unroll
+    for (int j = 0; j < NFW; ++j) frag[j] = tile_n * FR + wave * NFW + j;
+  }
+  const half8* W[NFW];
+#pragma unroll
+  for (int j = 0; j < NFW; ++j) W[j] = reinterpret_cast<const half8*>(a.w_hi) + (size_t)frag[j] * frag_stride + lane;
+  const half8* X = reinterpret_cast<const half8*>(a.x_hi);
+
+  floatx4 acc[MF][NFW];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int j = 0; j < NFW; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  half8 stage[PIECES];
+  auto fetch_x = [&](int c) {
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int e = threadIdx.x + q * NT;  // (i, j, lane) flattened
+      if (e < CHUNK) {
+        const int ln = e & 63, j = (e >> 6) % KC, i = e / (64 * KC);
+        const int kt = kt0 + c * KC + j;
+        stage[q] = kt < kt1 ? X[(size_t)i * frag_stride + (size_t)kt * 64 + ln] : half8{};
+      }
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PIECES; ++q) {
+      const int e = threadIdx.x + q * NT;
+      if (e < CHUNK) xs[buf * CHUNK + e] = stage[q];
+    }
+  };
+  half8 rb[P][NFW];
+  // Unconditional weight loads (see gemm_kernel); past the range they re-read the last k-step.
+  const int kt_last = max(0, min(kt1, KT) - 1);
+  auto load_w = [&](int slot, int kt) {
+    kt = min(kt, kt_last);
+#pragma unroll
+    for (int j = 0; j < NFW; ++j) rb[slot][j] = __builtin_nontemporal_load(W[j] + (size_t)kt * 64);
+  };
+#pragma unroll
+  for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
+  if (chunks > 0) {
+    fetch_x(0);
+    store_x(0);
+  }
+  __syncthreads();
+  for (int c = 0; c < chunks; ++c) {
+    if (c + 1 < chunks) fetch_x(c + 1);
+    const half8* xb = xs + (c & 1) * CHUNK;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int step = c * KC + j;
+      const int slot = j % P;
+      if (step < steps) {
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          const half8 x = xb[(i * KC + j) * 64 + lane];
+#pragma unroll
+          for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[slot][n], x, acc[i][n]);
+        }
+      }
+      load_w(slot, kt0 + step + P);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c + 1 < chunks) store_x((c + 1) & 1);
+    __syncthreads();
+  }
+
+  // Lane (q = lane / 16, t = lane % 16) of accumulator (i, n) holds row 16 i + t, features
+  // 16 frag[n] + 4 q .. + 3.
+  const int q4 = (lane >> 4) * 4, t16 = lane & 15;
+  if constexpr (PAIR) {
+    const int group = tile_n * (FR / 4) + (wave >> 1), h = wave & 1;
+    const uint64_t col = (uint64_t)group * 32 + h * 16 + q4;
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const int row = i * 16 + t16;
+      if (row >= M || col >= a.out_cols_padded) continue;
+      half4 vh;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) vh[t] = to_half(silu_mul(acc[i][0][t], acc[i][1][t]));
+      *reinterpret_cast<half4*>(a.out_hi + flayout_index(row, col, a.out_cols_padded)) = vh;
+    }
+    return;
+  }
+  const bool partial = a.ksplit > 1;  // deferred: a row-major [M][N] matrix per K split
+  float* base = partial ? a.workspace + (size_t)split * a.M * a.N : a.out;
+  const int ld = partial ? a.N : a.ldo;
+  const bool vec = (a.N & 3) == 0 && (ld & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+    const int row = i * 16 + t16;
+    if (row >= M) continue;
+#pragma unroll
+    for (int n = 0; n < NFW; ++n) {
+      const int col = frag[n] * 16 + q4;
+      if (col >= a.N) continue;
+      const floatx4 v = acc[i][n];
+      float* dst = base + (size_t)row * ld + col;
+      if (!partial && a.epilogue == kEpiResidual) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (col + t < a.N) dst[t] += v[t];
+      } else if (vec && col + 3 < a.N) {
+        *reinterpret_cast<floatx4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (col + t < a.N) dst[t] = v[t];
+      }
+    }
+  }
+}
+
+// Launches the decode kernel with `waves` waves per workgroup (4, 8 or 16) and the given
+// K split; returns the number of deferred partials (0: the epilogue has been applied).
+template <int MF, int NFW, int KC, int P, bool PAIR>
+int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
+  const int fr = waves * NFW;
+  const int n_tiles = (a.N + 16 * fr - 1) / (16 * fr);
+  if ((uint64_t)n_tiles * fr * 16 > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
+  if ((uint64_t)MF * 16 > a.x_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the activation padding");
+  if (ksplit > 1 && (!a.defer_reduce || PAIR)) fail(HLLM_INTERNAL, "decode GEMM splits K only for deferred consumers");
+  if (ksplit > 1 && (size_t)ksplit * a.M * a.N > a.workspace_floats) ksplit = 1;
+  a.ksplit = ksplit;
+  const size_t lds = 2 * (size_t)MF * KC * 64 * 16;
+  const dim3 grid((unsigned)(n_tiles * ksplit));
+  auto go = [&](auto kernel, const char* name) {
+    static const bool configured = [kernel] {
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      return true;
+    }();
+    (void)configured;
+    observed(name, [&] { kernel<<<grid, 64 * waves, lds, stream>>>(a, n_tiles); });
+  };
+  if (waves >= 8)
+    go(&gemm_decode_kernel<MF, 8, NFW, KC, P, PAIR>, kernel_name<MF, 8, NFW, KC, P, PAIR ? 1 : 0>("gemm_decode_kernel"));
+  else
+    go(&gemm_decode_kernel<MF, 4, NFW, KC, P, PAIR>, kernel_name<MF, 4, NFW, KC, P, PAIR ? 1 : 0>("gemm_decode_kernel"));
+  return ksplit > 1 ? ksplit : 0;
+}
+
 // Configuration table (ids are stable for the tuning harness):
 //   0..2: decode, BM = 16/32/64, BN = 64, four K-waves, ring of 4 k-steps
 //   3:    prefill, 128 x 128, 2 x 2 waves, ring of 2 k-steps
@@ -1095,6 +1274,80 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred) {
 }  // namespace
 
 namespace {
+
+int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : fallback;
+}
+
+// The decode kernel's launch shapes, from sweeps of the Qwen3-4B decode projections at 64
+// rows (weights streamed from HBM, launches back to back): waves per workgroup, the waves per
+// CU the K split aims at, the weight ring depth, the staged chunk (k-steps) and the fragment
+// rows per wave. Deferred projections: eight waves of one fragment row, chunks of four;
+// gate/up pairs: four waves, chunks of eight. HLLM_ROCM_DECODE_WAVES / _TARGET / _RING /
+// _CHUNK / _FRAGS override the deferred shape, HLLM_ROCM_DECODE_PAIR_WAVES / _PAIR_CHUNK the
+// paired one, for sweeps.
+struct DecodeShape {
+  int waves, target_waves_per_cu, ring, chunk, frags;
+};
+const DecodeShape& decode_shape(bool pair) {
+  static const DecodeShape deferred{env_int("HLLM_ROCM_DECODE_WAVES", 8), env_int("HLLM_ROCM_DECODE_TARGET", 6),
+                                    env_int("HLLM_ROCM_DECODE_RING", 4), env_int("HLLM_ROCM_DECODE_CHUNK", 4),
+                                    env_int("HLLM_ROCM_DECODE_FRAGS", 1)};
+  static const DecodeShape paired{env_int("HLLM_ROCM_DECODE_PAIR_WAVES", 4), 0, 8,
+                                  env_int("HLLM_ROCM_DECODE_PAIR_CHUNK", 8), 2};
+  return pair ? paired : deferred;
+}
+
+// Whether the decode kernel runs this projection: F16, at most 64 rows, and either a consumer
+// that sums K splits, SwiGLU (never split), or enough output features to fill the GPU unsplit.
+bool decode_applies(const GemmArgs& a, int prec, int rows, int cus) {
+  if (prec != kF16 || rows > 64 || rows <= 0) return false;
+  if (a.defer_reduce || a.epilogue == kEpiSwiglu) return true;
+  const int waves = decode_shape(false).waves >= 8 ? 8 : 4;
+  const int n_tiles = (a.N + 16 * waves - 1) / (16 * waves);
+  return n_tiles * waves >= 4 * cus;
+}
+
+template <int MF, int KC, int P>
+int launch_decode_variant(hipStream_t stream, const GemmArgs& a, int cus) {
+  const bool pair = a.epilogue == kEpiSwiglu;
+  const DecodeShape& d = decode_shape(pair);
+  const int chunks = (int)((a.Kp >> 5) + KC - 1) / KC;
+  const int waves = d.waves >= 8 ? 8 : 4;
+  int nfw = pair ? 2 : (d.frags >= 4 ? 4 : d.frags >= 2 ? 2 : 1);
+  // Tiles never read past the weight rows (padded to 256).
+  while (nfw > 1 && !pair && (uint64_t)((a.N + 16 * waves * nfw - 1) / (16 * waves * nfw)) * waves * nfw * 16 > a.w_rows_padded)
+    nfw /= 2;
+  const int fr = waves * nfw;
+  const int n_tiles = (a.N + 16 * fr - 1) / (16 * fr);
+  int ksplit = 1;
+  if (a.defer_reduce) {
+    // Splits of whole chunks, none of them empty.
+    const double want = (double)d.target_waves_per_cu * cus / ((double)n_tiles * waves);
+    ksplit = std::max(1, std::min((int)(want + 0.5), chunks / 2 > 0 ? chunks / 2 : 1));
+    const int per = (chunks + ksplit - 1) / ksplit;
+    ksplit = (chunks + per - 1) / per;
+  }
+  if (pair) return launch_decode_waves<MF, 2, KC, P, true>(stream, a, waves, 1);
+  if (nfw == 4) return launch_decode_waves<MF, 4, KC, P, false>(stream, a, waves, ksplit);
+  if (nfw == 2) return launch_decode_waves<MF, 2, KC, P, false>(stream, a, waves, ksplit);
+  return launch_decode_waves<MF, 1, KC, P, false>(stream, a, waves, ksplit);
+}
+
+template <int MF>
+int launch_decode_rows(hipStream_t stream, const GemmArgs& a, int cus) {
+  const DecodeShape& d = decode_shape(a.epilogue == kEpiSwiglu);
+  if (d.chunk <= 4) return launch_decode_variant<MF, 4, 4>(stream, a, cus);
+  return launch_decode_variant<MF, 8, 8>(stream, a, cus);
+}
+
+int launch_decode(hipStream_t stream, const GemmArgs& a, int rows, int cus) {
+  if (rows <= 16) return launch_decode_rows<1>(stream, a, cus);
+  if (rows <= 32) return launch_decode_rows<2>(stream, a, cus);
+  return launch_decode_rows<4>(stream, a, cus);
+}
+
 std::atomic<int>& forced_config() {
   static std::atomic<int> forced{[] {
     const char* v = std::getenv("HLLM_ROCM_GEMM_CONFIG");
@@ -1108,9 +1361,13 @@ int set_forced_gemm_config(int config) { return forced_config().exchange(config)
 
 int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
   if (rows_bound <= 0) return 0;
-  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0);
   const int forced = forced_config().load(std::memory_order_relaxed);
-  if (forced >= 0) c = {forced, 0};
+  if (forced < 0 && env_int("HLLM_ROCM_DECODE_OFF", 0) == 0 && decode_applies(args, prec, rows_bound, cus))
+    return launch_decode(stream, args, rows_bound, cus);
+  if (forced == kDecodeConfig && prec == kF16 && rows_bound <= 64 && (args.defer_reduce || args.epilogue == kEpiSwiglu))
+    return launch_decode(stream, args, rows_bound, cus);
+  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0);
+  if (forced >= 0 && forced != kDecodeConfig) c = {forced, 0};
   return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }
 

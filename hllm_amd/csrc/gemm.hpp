@@ -46,7 +46,10 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
 int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
                         int config, int forced_ksplit);
 // Highest configuration id of the table.
-constexpr int kGemmConfigs = 16;
+constexpr int kGemmConfigs = 17;
+// Forced configuration meaning "the decode kernel wherever it applies" (F16, at most 64 rows,
+// deferred K splits or SwiGLU); other projections keep the choice by shape.
+constexpr int kDecodeConfig = 17;
 // Process-wide override of the configuration choice for every later launch_gemm (-1: the
 // choice by shape; initially HLLM_ROCM_GEMM_CONFIG when set). Returns the previous value.
 int set_forced_gemm_config(int config);

@@ -63,7 +63,7 @@ def stage():
     st.close()
 
 
-@pytest.mark.parametrize("config", [9, 14, 15, 16])
+@pytest.mark.parametrize("config", [9, 14, 15, 16, 17])
 def test_forced_configuration_matches_the_oracle(stage, expected, config):
     prompts, first, logits, tokens, second = expected
     _say("gemm configuration", config)

@@ -5,7 +5,8 @@ with the full vocabulary, against the F32 CPU oracle:
 * one pass of 64 decode rows at lognormal contexts (median 256, sigma 1, clipped to
   [16, 2048]) with the projection GEMMs chosen by shape, and with each of the decode
   configurations forced (0, 1, 2: register-streaming tiles of 16/32/64 rows; 12:
-  activation-staged 64 x 256 tiles, the choice for gate+up and the LM head at 33-64 rows);
+  activation-staged 64 x 256 tiles; 17: the decode kernel, one weight stream per wave with
+  gate/up pairs and a SwiGLU register epilogue);
 * one pass mixing a 512-token prefill chunk of a new sequence with the same 64 decode rows.
 
 Per row: last-layer hidden state and logits within max-abs 2e-2 and cosine 0.9999."""
@@ -74,7 +75,7 @@ def _decode_items(seqs, lengths):
     return [capi.item(s, 1, n) for s, n in zip(seqs, lengths)]
 
 
-@pytest.mark.parametrize("config", [-1, 0, 1, 2, 12])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 12, 17])
 def test_64_decode_rows_match_the_oracle(world, config):
     w, st = world, world["stage"]
     hp.say("qwen3-4b 64 decode rows, gemm configuration", config)
