@@ -258,6 +258,12 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
       }
     }
   }
+  // The norm weights are loaded before the reduction, so their latency overlaps it.
+  float wv[Q][8];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[q][j] = c0[q] + j < hidden ? weight[c0[q] + j] : 0.0f;
   float squares = 0.0f;
 #pragma unroll
   for (int q = 0; q < Q; ++q)
@@ -272,7 +278,7 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int cc = c0[q] + j;
-      const float y = cc < hidden ? (v[q][j] * inverse) * weight[cc] : 0.0f;
+      const float y = cc < hidden ? (v[q][j] * inverse) * wv[q][j] : 0.0f;
       vh[j] = to_half(y);
       vl[j] = to_half((y - (float)vh[j]) * kLoScale);
     }

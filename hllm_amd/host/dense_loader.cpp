@@ -5,6 +5,7 @@
 #include <fstream>
 #include <set>
 #include <sstream>
+#include <string_view>
 
 #include "json.hpp"
 
@@ -14,14 +15,44 @@ using runtime::Error;
 
 namespace {
 
-struct Expected {
-  std::vector<std::size_t> shape;
-  TensorRole role;
-  int layer;  // -1 for non-layer tensors
+// The model families a dense stage runs, by manifest architecture id; revision "1" only.
+struct Family {
+  std::string_view id;
+  bool query_key_norm;  // carries per-head q/k norms and must declare "qk_norm"
+};
+constexpr Family kFamilies[] = {{"llama.v1", false}, {"qwen3.v1", true}};
+// Feature flags any family may declare; they change nothing the stage computes.
+constexpr std::string_view kNeutralFeatures[] = {"gqa", "mha", "tied_embeddings", "untied_embeddings",
+                                                 "explicit_head_dim"};
+
+// Dimensions a tensor's shape is written in.
+enum class Dim { kNone, kHidden, kIntermediate, kQueryWidth, kKeyValueWidth, kHeadDim, kVocabulary };
+
+// The tensors of one transformer layer, as "model.layers.<i>." + suffix; a vector has one
+// dimension (cols kNone).
+struct LayerTensor {
+  std::string_view suffix;
+  Dim rows, cols;
+  bool query_key_norm_only;
+};
+constexpr LayerTensor kLayerTensors[] = {
+    {"input_layernorm.weight", Dim::kHidden, Dim::kNone, false},
+    {"self_attn.q_proj.weight", Dim::kQueryWidth, Dim::kHidden, false},
+    {"self_attn.k_proj.weight", Dim::kKeyValueWidth, Dim::kHidden, false},
+    {"self_attn.v_proj.weight", Dim::kKeyValueWidth, Dim::kHidden, false},
+    {"self_attn.q_norm.weight", Dim::kHeadDim, Dim::kNone, true},
+    {"self_attn.k_norm.weight", Dim::kHeadDim, Dim::kNone, true},
+    {"self_attn.o_proj.weight", Dim::kHidden, Dim::kQueryWidth, false},
+    {"post_attention_layernorm.weight", Dim::kHidden, Dim::kNone, false},
+    {"mlp.gate_proj.weight", Dim::kIntermediate, Dim::kHidden, false},
+    {"mlp.up_proj.weight", Dim::kIntermediate, Dim::kHidden, false},
+    {"mlp.down_proj.weight", Dim::kHidden, Dim::kIntermediate, false},
 };
 
+[[noreturn]] void refuse(const std::string& why) { throw Error::incompatible_worker("stage not admitted: " + why); }
+
 std::size_t mul(std::size_t a, std::size_t b) {
-  if (b != 0 && a > SIZE_MAX / b) throw Error::resource_exhausted("size overflow");
+  if (b != 0 && a > SIZE_MAX / b) refuse("a tensor size overflows");
   return a * b;
 }
 
@@ -39,158 +70,240 @@ WireDType wire_type(runtime::DataType d) {
   }
 }
 
-// A file name with no directory part, resolving to a file directly inside `root`.
-bool confined(const std::filesystem::path& root, const std::string& file) {
-  const std::filesystem::path rel(file);
-  if (rel.empty() || rel.is_absolute() || rel.has_parent_path() || rel == "." || rel == "..") return false;
+// A bare file name naming a file that resolves (links included) directly inside `root`.
+bool inside(const std::filesystem::path& root, const std::string& file) {
+  const std::filesystem::path name(file);
+  if (name.empty() || name.is_absolute() || name.has_parent_path() || name == "." || name == "..") return false;
   std::error_code ec;
-  const auto target = std::filesystem::canonical(root / rel, ec);
+  const auto target = std::filesystem::canonical(root / name, ec);
   if (ec) return false;
   const auto base = std::filesystem::canonical(root, ec);
   return !ec && target.parent_path() == base;
 }
 
-}  // namespace
+// One tensor the stage needs, with the record role and layer index it must carry.
+struct Slot {
+  std::string name;
+  TensorRole role;
+  std::optional<std::uint32_t> layer;
+  std::vector<std::size_t> shape;
+  bool uploaded{true};  // false: a serialized head beside tied embeddings, checked, never held
+};
 
-DenseSource inspect_dense_stage(const LoadStageRequest& request, const std::filesystem::path& root) {
-  const DeploymentPlan& plan = request.plan;
-  if (request.stage_index >= plan.stages.size() ||
-      (plan.execution_dtype != WireDType::kF32 && plan.execution_dtype != WireDType::kF16))
-    throw Error::incompatible_worker("invalid stage index or unsupported execution dtype");
-  const bool mixed = plan.weight_dtype.has_value();
-  if (mixed != (plan.schema_major == 1 && plan.schema_minor == 2) ||
-      (mixed && (*plan.weight_dtype != WireDType::kF16 || plan.execution_dtype != WireDType::kF32)))
-    throw Error::incompatible_worker("unsupported resident/execution precision contract");
+// Admission of one LoadStageRequest, rule group by rule group; every failure is
+// INCOMPATIBLE_WORKER.
+class Admission {
+ public:
+  Admission(const LoadStageRequest& request, const std::filesystem::path& root)
+      : request_(request), plan_(request.plan), manifest_(request.manifest), config_(request.manifest.config),
+        root_(root) {}
 
-  const ModelManifest& manifest = request.manifest;
-  const ArchitectureDescriptor& arch = manifest.architecture;
-  const bool known = arch.architecture_id == "llama.v1" || arch.architecture_id == "qwen3.v1";
-  if (!known || arch.architecture_revision != "1")
-    throw Error::incompatible_worker("unsupported architecture ID or revision");
-  const bool qwen = arch.architecture_id == "qwen3.v1";
-  static const std::set<std::string> kFeatures{"gqa", "mha", "tied_embeddings", "untied_embeddings",
-                                               "explicit_head_dim"};
-  bool qk_norm = false;
-  for (const std::string& f : arch.feature_flags) {
-    if (qwen && f == "qk_norm")
-      qk_norm = true;
-    else if (!kFeatures.count(f))
-      throw Error::incompatible_worker("unsupported architecture feature: " + f);
+  DenseSource run() {
+    precision();
+    const Family& family = architecture();
+    configuration();
+    const StageAssignment& stage = assignment();
+    fill_source(family, stage);
+    index_records();
+    const std::vector<Slot> slots = slots_for(family, stage);
+    no_unexpected_selection(slots, stage);
+    for (const Slot& slot : slots) bind(slot);
+    if (src_.tied_head && records_.count("lm_head.weight")) redundant_head();
+    return std::move(src_);
   }
-  if (qwen && !qk_norm) throw Error::incompatible_worker("Qwen3 requires qk_norm feature");
 
-  const ModelConfig& c = manifest.config;
-  const bool shape_ok = c.hidden_size && c.intermediate_size && c.num_layers && c.num_attention_heads &&
-                        c.num_kv_heads && c.head_dim && c.head_dim % 2 == 0 &&
-                        c.num_attention_heads % c.num_kv_heads == 0 && c.maximum_sequence_length &&
-                        c.vocabulary_size;
-  const bool math_ok = c.hidden_activation == "silu" && !c.attention_bias && !c.mlp_bias && !c.has_rope_scaling &&
-                       std::isfinite(c.rms_norm_eps) && c.rms_norm_eps > 0 && std::isfinite(c.rope_theta) &&
-                       c.rope_theta > 0 && std::isfinite(static_cast<float>(c.rope_theta)) &&
-                       std::isfinite(static_cast<float>(c.rms_norm_eps)) && static_cast<float>(c.rms_norm_eps) > 0;
-  if (!shape_ok || !math_ok) throw Error::incompatible_worker("unsupported dense model configuration");
+ private:
+  // Execution F32 or F16; F16 weights under F32 execution exactly when the plan is schema 1.2.
+  void precision() {
+    const WireDType exec = plan_.execution_dtype;
+    if (exec != WireDType::kF32 && exec != WireDType::kF16) refuse("execution precision must be F32 or F16");
+    const bool schema_1_2 = plan_.schema_major == 1 && plan_.schema_minor == 2;
+    if (plan_.weight_dtype.has_value() != schema_1_2)
+      refuse("a resident weight precision is given exactly by schema 1.2 plans");
+    if (plan_.weight_dtype && (*plan_.weight_dtype != WireDType::kF16 || exec != WireDType::kF32))
+      refuse("mixed residency holds F16 weights under F32 execution only");
+    mixed_ = plan_.weight_dtype.has_value();
+  }
 
-  const StageAssignment& stage = plan.stages[request.stage_index];
-  const std::size_t per_layer = qwen ? 11 : 9;
-  if (stage.layer_start >= stage.layer_end || stage.layer_end > c.num_layers ||
-      stage.layer_end - stage.layer_start > manifest.tensors.size() / per_layer)
-    throw Error::incompatible_worker("layer range exceeds available tensor records");
-  const bool first = request.stage_index == 0;
-  const bool final = request.stage_index + 1 == plan.stages.size();
-  if (stage.owns_token_embedding != first || stage.owns_sampling != final || stage.owns_final_norm != final ||
-      stage.owns_lm_head != final)
-    throw Error::incompatible_worker("inconsistent stage tensor ownership");
+  const Family& architecture() {
+    const ArchitectureDescriptor& a = manifest_.architecture;
+    const Family* family = nullptr;
+    for (const Family& f : kFamilies)
+      if (a.architecture_id == f.id) family = &f;
+    if (!family || a.architecture_revision != "1")
+      refuse("architecture " + a.architecture_id + " revision " + a.architecture_revision + " is not served");
+    bool declares_qk_norm = false;
+    for (const std::string& flag : a.feature_flags) {
+      if (family->query_key_norm && flag == "qk_norm") {
+        declares_qk_norm = true;
+        continue;
+      }
+      if (std::find(std::begin(kNeutralFeatures), std::end(kNeutralFeatures), flag) == std::end(kNeutralFeatures))
+        refuse("feature " + flag + " is not served");
+    }
+    if (family->query_key_norm && !declares_qk_norm) refuse(a.architecture_id + " must declare qk_norm");
+    return *family;
+  }
 
-  DenseSource src;
-  src.config = {c.hidden_size,
-                c.intermediate_size,
-                c.num_attention_heads,
-                c.num_kv_heads,
-                c.head_dim,
-                c.maximum_sequence_length,
-                static_cast<float>(c.rms_norm_eps),
-                static_cast<float>(c.rope_theta),
-                qwen};
-  src.vocabulary_size = c.vocabulary_size;
-  src.first = first;
-  src.final = final;
-  src.layer_start = stage.layer_start;
-  src.layer_end = stage.layer_end;
-  src.tied_head = stage.owns_lm_head && c.tied_embeddings;
-  src.execution_dtype = storage_type(plan.execution_dtype);
-  src.weight_dtype = mixed ? runtime::DataType::kF16 : src.execution_dtype;
+  void configuration() {
+    const ModelConfig& c = config_;
+    const bool dims = c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0 && c.num_attention_heads > 0 &&
+                      c.num_kv_heads > 0 && c.head_dim > 0 && c.maximum_sequence_length > 0 &&
+                      c.vocabulary_size > 0;
+    if (!dims) refuse("a model dimension is zero");
+    if (c.head_dim % 2 != 0) refuse("rotary embedding needs an even head dimension");
+    if (c.num_attention_heads % c.num_kv_heads != 0) refuse("query heads must group evenly over key/value heads");
+    if (c.hidden_activation != "silu" || c.attention_bias || c.mlp_bias || c.has_rope_scaling)
+      refuse("only SiLU MLPs without biases and unscaled rotary embedding are served");
+    // Both constants are used as F32 on the device: positive and finite there, and the
+    // epsilon must not round to zero.
+    auto finite_positive = [](double v) { return std::isfinite(v) && v > 0 && std::isfinite(static_cast<float>(v)); };
+    if (!finite_positive(c.rms_norm_eps) || static_cast<float>(c.rms_norm_eps) <= 0 || !finite_positive(c.rope_theta))
+      refuse("norm epsilon and rope theta must be positive and finite as F32");
+  }
 
-  const std::size_t H = c.hidden_size, I = c.intermediate_size;
-  const std::size_t QD = mul(c.num_attention_heads, c.head_dim), KD = mul(c.num_kv_heads, c.head_dim);
-  std::map<std::string, Expected> expected;
-  if (stage.owns_token_embedding || src.tied_head)
-    expected["model.embed_tokens.weight"] = {{c.vocabulary_size, H}, TensorRole::kTokenEmbedding, -1};
-  if (stage.owns_final_norm) expected["model.norm.weight"] = {{H}, TensorRole::kFinalNorm, -1};
-  if (stage.owns_lm_head && !c.tied_embeddings)
-    expected["lm_head.weight"] = {{c.vocabulary_size, H}, TensorRole::kLmHead, -1};
-  for (std::uint32_t l = stage.layer_start; l < stage.layer_end; ++l) {
-    const std::string p = "model.layers." + std::to_string(l) + ".";
-    const int li = static_cast<int>(l);
-    const std::pair<const char*, std::vector<std::size_t>> shapes[] = {
-        {"input_layernorm.weight", {H}},      {"post_attention_layernorm.weight", {H}},
-        {"self_attn.q_proj.weight", {QD, H}}, {"self_attn.k_proj.weight", {KD, H}},
-        {"self_attn.v_proj.weight", {KD, H}}, {"self_attn.o_proj.weight", {H, QD}},
-        {"mlp.gate_proj.weight", {I, H}},     {"mlp.up_proj.weight", {I, H}},
-        {"mlp.down_proj.weight", {H, I}}};
-    for (const auto& [n, s] : shapes) expected[p + n] = {s, TensorRole::kTransformerLayer, li};
-    if (qwen) {
-      expected[p + "self_attn.q_norm.weight"] = {{c.head_dim}, TensorRole::kTransformerLayer, li};
-      expected[p + "self_attn.k_norm.weight"] = {{c.head_dim}, TensorRole::kTransformerLayer, li};
+  // The stage's layers lie in the model; the first stage alone owns the embedding, the
+  // last alone the final norm, the head and sampling.
+  const StageAssignment& assignment() {
+    if (request_.stage_index >= plan_.stages.size()) refuse("stage index outside the plan");
+    const StageAssignment& s = plan_.stages[request_.stage_index];
+    if (s.layer_start >= s.layer_end || s.layer_end > config_.num_layers) refuse("empty or out-of-model layer range");
+    const bool first = request_.stage_index == 0, last = request_.stage_index + 1 == plan_.stages.size();
+    if (s.owns_token_embedding != first || s.owns_final_norm != last || s.owns_lm_head != last ||
+        s.owns_sampling != last)
+      refuse("tensor ownership does not follow the stage's place in the plan");
+    return s;
+  }
+
+  void fill_source(const Family& family, const StageAssignment& s) {
+    const ModelConfig& c = config_;
+    src_.config = {c.hidden_size,        c.intermediate_size,
+                   c.num_attention_heads, c.num_kv_heads,
+                   c.head_dim,            c.maximum_sequence_length,
+                   static_cast<float>(c.rms_norm_eps), static_cast<float>(c.rope_theta),
+                   family.query_key_norm};
+    src_.vocabulary_size = c.vocabulary_size;
+    src_.first = s.owns_token_embedding;
+    src_.final = s.owns_sampling;
+    src_.layer_start = s.layer_start;
+    src_.layer_end = s.layer_end;
+    src_.tied_head = s.owns_lm_head && c.tied_embeddings;
+    src_.execution_dtype = storage_type(plan_.execution_dtype);
+    src_.weight_dtype = mixed_ ? runtime::DataType::kF16 : src_.execution_dtype;
+  }
+
+  void index_records() {
+    for (const TensorRecord& r : manifest_.tensors)
+      if (!records_.emplace(r.name, &r).second) refuse("the manifest lists " + r.name + " twice");
+  }
+
+  std::size_t extent(Dim d) const {
+    const ModelConfig& c = config_;
+    switch (d) {
+      case Dim::kHidden: return c.hidden_size;
+      case Dim::kIntermediate: return c.intermediate_size;
+      case Dim::kQueryWidth: return mul(c.num_attention_heads, c.head_dim);
+      case Dim::kKeyValueWidth: return mul(c.num_kv_heads, c.head_dim);
+      case Dim::kHeadDim: return c.head_dim;
+      case Dim::kVocabulary: return c.vocabulary_size;
+      case Dim::kNone: break;
+    }
+    return 0;
+  }
+
+  std::vector<Slot> slots_for(const Family& family, const StageAssignment& s) const {
+    std::vector<Slot> slots;
+    const std::vector<std::size_t> table{extent(Dim::kVocabulary), extent(Dim::kHidden)};
+    // The embedding serves the first stage's lookup and, tied, the last stage's head.
+    if (s.owns_token_embedding || src_.tied_head)
+      slots.push_back({"model.embed_tokens.weight", TensorRole::kTokenEmbedding, std::nullopt, table});
+    for (std::uint32_t l = s.layer_start; l < s.layer_end; ++l)
+      for (const LayerTensor& t : kLayerTensors) {
+        if (t.query_key_norm_only && !family.query_key_norm) continue;
+        std::vector<std::size_t> shape{extent(t.rows)};
+        if (t.cols != Dim::kNone) shape.push_back(extent(t.cols));
+        slots.push_back({"model.layers." + std::to_string(l) + "." + std::string(t.suffix),
+                         TensorRole::kTransformerLayer, l, std::move(shape)});
+      }
+    if (s.owns_final_norm) slots.push_back({"model.norm.weight", TensorRole::kFinalNorm, std::nullopt, {table[1]}});
+    if (s.owns_lm_head && (!config_.tied_embeddings || records_.count("lm_head.weight")))
+      slots.push_back({"lm_head.weight", TensorRole::kLmHead, std::nullopt, table, !config_.tied_embeddings});
+    return slots;
+  }
+
+  // Every record the stage's ownership selects (its layers, and the embedding, final norm
+  // or untied head it owns) must be one of its slots.
+  void no_unexpected_selection(const std::vector<Slot>& slots, const StageAssignment& s) const {
+    std::set<std::string_view> wanted;
+    for (const Slot& slot : slots) wanted.insert(slot.name);
+    for (const auto& [name, r] : records_) {
+      bool selected = false;
+      switch (r->role) {
+        case TensorRole::kTransformerLayer:
+          selected = r->layer_index && *r->layer_index >= s.layer_start && *r->layer_index < s.layer_end;
+          break;
+        case TensorRole::kTokenEmbedding: selected = s.owns_token_embedding; break;
+        case TensorRole::kFinalNorm: selected = s.owns_final_norm; break;
+        case TensorRole::kLmHead: selected = s.owns_lm_head && !config_.tied_embeddings; break;
+        default: break;
+      }
+      if (selected && !wanted.count(name)) refuse(name + " is not a tensor this stage runs");
     }
   }
 
-  std::map<std::string, const TensorRecord*> records;
-  for (const TensorRecord& r : manifest.tensors)
-    if (!records.emplace(r.name, &r).second) throw Error::incompatible_worker("duplicate tensor in manifest");
-  // A serialized head beside tied embeddings is checked against the embedding, never held.
-  const bool redundant_head = src.tied_head && records.count("lm_head.weight");
-  if (redundant_head) expected["lm_head.weight"] = {{c.vocabulary_size, H}, TensorRole::kLmHead, -1};
-  for (const auto& [name, r] : records) {
-    const bool owned =
-        (r->role == TensorRole::kTransformerLayer && r->layer_index && *r->layer_index >= stage.layer_start &&
-         *r->layer_index < stage.layer_end) ||
-        (r->role == TensorRole::kTokenEmbedding && stage.owns_token_embedding) ||
-        (r->role == TensorRole::kFinalNorm && stage.owns_final_norm) ||
-        (r->role == TensorRole::kLmHead && stage.owns_lm_head && !c.tied_embeddings);
-    if (owned && !expected.count(name)) throw Error::incompatible_worker("unsupported selected tensor: " + name);
+  // The slot's record (role, layer, shape) and its Safetensors entry (element type, shape,
+  // offset, length) must agree; the file must lie in the model root.
+  void bind(const Slot& slot) {
+    const auto found = records_.find(slot.name);
+    if (found == records_.end()) refuse("the manifest lacks " + slot.name);
+    const TensorRecord& r = *found->second;
+    if (r.role != slot.role || r.layer_index != slot.layer || r.shape != slot.shape)
+      refuse(slot.name + " has the wrong role, layer or shape");
+    if (!inside(root_, r.file)) refuse(slot.name + " names a file outside the model root");
+    auto file = src_.files.find(r.file);
+    if (file == src_.files.end()) file = src_.files.emplace(r.file, runtime::SafetensorsFile(root_ / r.file)).first;
+    const runtime::TensorMetadata& stored = file->second.tensor(slot.name);
+    const WireDType stored_type = wire_type(stored.dtype);
+    if (stored_type == WireDType::kUnspecified) refuse(slot.name + " is stored in an unsupported element type");
+    if (stored_type != r.dtype || stored.shape != slot.shape || stored.data_offset != r.data_offset ||
+        stored.byte_length != r.byte_length)
+      refuse(slot.name + ": the manifest record and the Safetensors header disagree");
+    if (!slot.uploaded) return;
+    std::size_t elements = 1;
+    for (std::size_t d : slot.shape) elements = mul(elements, d);
+    // Norm vectors stay F32; matrices are held in the resident weight precision.
+    const std::size_t held = slot.shape.size() == 1 || src_.weight_dtype == runtime::DataType::kF32 ? 4 : 2;
+    src_.resident_bytes += mul(elements, held);
+    src_.largest_payload_bytes = std::max(src_.largest_payload_bytes, stored.byte_length);
+    src_.tensors.emplace(slot.name, TensorSource{r.file, slot.shape, stored.dtype});
   }
 
-  const std::size_t resident_element = src.weight_dtype == runtime::DataType::kF32 ? 4 : 2;
-  for (const auto& [name, want] : expected) {
-    const auto hit = records.find(name);
-    if (hit == records.end()) throw Error::incompatible_worker("missing required tensor: " + name);
-    const TensorRecord& r = *hit->second;
-    const bool layer_ok = want.layer >= 0 ? (r.layer_index && *r.layer_index == static_cast<std::uint32_t>(want.layer))
-                                          : !r.layer_index.has_value();
-    if (r.role != want.role || !layer_ok || r.shape != want.shape)
-      throw Error::incompatible_worker("incorrect tensor shape or ownership: " + name);
-    if (!confined(root, r.file)) throw Error::incompatible_worker("tensor path escapes model root");
-    auto file = src.files.find(r.file);
-    if (file == src.files.end()) file = src.files.emplace(r.file, runtime::SafetensorsFile(root / r.file)).first;
-    const runtime::TensorMetadata& meta = file->second.tensor(name);
-    const WireDType stored = wire_type(meta.dtype);
-    if (stored == WireDType::kUnspecified || r.dtype != stored || meta.shape != want.shape ||
-        meta.data_offset != r.data_offset || meta.byte_length != r.byte_length)
-      throw Error::incompatible_worker("Safetensors metadata mismatch or unsupported dtype: " + name);
-    if (redundant_head && name == "lm_head.weight") continue;
-    std::size_t elements = 1;
-    for (std::size_t d : want.shape) elements = mul(elements, d);
-    src.resident_bytes += mul(elements, want.shape.size() == 1 ? 4 : resident_element);
-    src.largest_payload_bytes = std::max(src.largest_payload_bytes, meta.byte_length);
-    src.tensors.emplace(name, TensorSource{r.file, want.shape, meta.dtype});
-  }
-  if (redundant_head) {
-    const auto& emb = src.files.at(records.at("model.embed_tokens.weight")->file).tensor("model.embed_tokens.weight");
-    const auto& head = src.files.at(records.at("lm_head.weight")->file).tensor("lm_head.weight");
+  // A serialized head beside tied embeddings is never used; it must be stored like the
+  // embedding it duplicates.
+  void redundant_head() const {
+    auto stored = [&](const std::string& name) -> const runtime::TensorMetadata& {
+      return src_.files.at(records_.at(name)->file).tensor(name);
+    };
+    const runtime::TensorMetadata& emb = stored("model.embed_tokens.weight");
+    const runtime::TensorMetadata& head = stored("lm_head.weight");
     if (emb.dtype != head.dtype || emb.shape != head.shape || emb.byte_length != head.byte_length)
-      throw Error::incompatible_worker("redundant tied head must match embedding storage metadata");
+      refuse("a serialized head beside tied embeddings must be stored like the embedding");
   }
-  return src;
+
+  const LoadStageRequest& request_;
+  const DeploymentPlan& plan_;
+  const ModelManifest& manifest_;
+  const ModelConfig& config_;
+  const std::filesystem::path& root_;
+  bool mixed_{false};
+  std::map<std::string, const TensorRecord*> records_;
+  DenseSource src_;
+};
+
+}  // namespace
+
+DenseSource inspect_dense_stage(const LoadStageRequest& request, const std::filesystem::path& root) {
+  return Admission(request, root).run();
 }
 
 namespace {

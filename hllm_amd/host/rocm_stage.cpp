@@ -2,6 +2,7 @@
 
 #include <cstring>
 #include <limits>
+#include <span>
 #include <unordered_set>
 
 namespace hllm_rocm::backend {
@@ -105,12 +106,10 @@ RocmStage::RocmStage(const model::DenseSource& source, const std::filesystem::pa
   (void)root;
   check(hllm_rocm_stage_create(&config_, &stage_));
   try {
-    std::vector<unsigned char> payload;
+    // Payloads go to the device straight from the files' read-only mappings.
     for (const auto& [name, t] : source.tensors) {
       const runtime::SafetensorsFile& file = source.files.at(t.file);
-      const runtime::TensorMetadata& meta = file.tensor(name);
-      payload.resize(meta.byte_length);
-      file.read(meta, 0, payload.data(), meta.byte_length);
+      const std::span<const std::byte> payload = file.payload(file.tensor(name));
       std::vector<std::uint64_t> shape(t.shape.begin(), t.shape.end());
       check(hllm_rocm_stage_load_tensor(stage_, name.c_str(), abi_dtype(t.dtype), shape.data(),
                                         static_cast<std::uint32_t>(shape.size()), payload.data(), payload.size()));

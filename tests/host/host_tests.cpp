@@ -127,11 +127,16 @@ void safetensors_reader() {
   CHECK(f.tensors().size() == 2 && f.tensors()[0].name == "a");
   const auto& b = f.tensor("b");
   CHECK(b.dtype == runtime::DataType::kF32 && b.shape == (std::vector<std::size_t>{2, 2}) && b.byte_length == 16);
+  const std::span<const std::byte> bytes = f.payload(b);
   float vals[4];
-  f.read(b, 0, vals, 16);
-  CHECK(vals[3] == 1.5f);
+  CHECK(bytes.size() == 16 && f.payload(f.tensor("a")).size() == 6);
+  std::memcpy(vals, bytes.data(), 16);
+  CHECK(vals[0] == 1.5f && vals[3] == 1.5f);
+  CHECK(std::to_integer<int>(f.payload(f.tensor("a"))[5]) == 1);
   EXPECT_ERROR(f.tensor("missing"), kIncompatibleWorker);
-  EXPECT_ERROR(f.read(b, 8, vals, 16), kIncompatibleWorker);
+  // The mapping moves with the file object.
+  runtime::SafetensorsFile moved(std::move(f));
+  CHECK(moved.tensors().size() == 2 && moved.payload(moved.tensor("b")).data() == bytes.data());
   const std::pair<std::string, std::string> bad[] = {
       {R"({"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}})", std::string(8, '\0')},     // length mismatch
       {R"({"x":{"dtype":"Q4","shape":[2],"data_offsets":[0,8]}})", std::string(8, '\0')},      // dtype
@@ -143,6 +148,10 @@ void safetensors_reader() {
       {R"({"__metadata__":{}})", ""},                                                          // no tensors
       {R"([1,2])", ""},                                                                        // not an object
       {R"({"x":)", ""},                                                                        // invalid JSON
+      {R"({"x":{"dtype":"F32","shape":[2.5],"data_offsets":[0,8]}})", std::string(8, '\0')},  // fractional dim
+      {R"({"x":{"dtype":"F32","shape":[2],"data_offsets":[0]}})", std::string(8, '\0')},      // one offset
+      {R"({"x":{"shape":[2],"data_offsets":[0,8]}})", std::string(8, '\0')},                  // no dtype
+      {R"({"x":7})", std::string(8, '\0')},                                                   // record not an object
   };
   int i = 0;
   for (const auto& [header, data] : bad) {
