@@ -27,6 +27,22 @@ namespace {
 
 constexpr int kXcds = 8;
 
+// Block -> (K split, weight tile, row tile) of the many-row kernels. Units (K split, weight
+// tile) are dealt round-robin to the eight XCDs (block b runs on XCD b % 8), and a unit's row
+// tiles are consecutive blocks of one XCD, so they share that XCD's L2 copy of the weight
+// tile and every XCD holds within one unit of the same work, whatever the tile count.
+struct TileCoord {
+  int split, tile_n, tile_m;
+  bool valid;
+};
+__device__ inline TileCoord xcd_tile(int block, int n_tiles, int m_tiles, int units) {
+  const int x = block % kXcds, j = block / kXcds;
+  const int local = j / m_tiles, tile_m = j - local * m_tiles;
+  const int u = local * kXcds + x;
+  return {u / n_tiles, u % n_tiles, tile_m, u < units};
+}
+inline unsigned xcd_grid(int units, int m_tiles) { return (unsigned)((units + kXcds - 1) / kXcds * kXcds * m_tiles); }
+
 __device__ inline floatx4 mfma(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -263,12 +279,11 @@ __global__ void __launch_bounds__(64 * WM * WN * WK)
 // LDS (chunks of KC k-steps, double-buffered) and read by all four waves, so activation
 // traffic per weight byte is BM / BN. Epilogues are applied straight from the accumulators.
 //
-// Block order is XCD-aware: id = split * slots + ((n_tile / 8) * m_tiles + m_tile) * 8 +
-// n_tile % 8, so all row tiles of one weight tile have the same id modulo 8 (one XCD, one
-// L2) and are dispatched together: the weight tile is read from HBM once.
+// Block order is XCD-aware (xcd_tile): the row tiles of one weight tile and K split run
+// together on one XCD, so the weight tile is read from HBM once.
 template <int MF, int NFW, int KC, int P, int PREC>
 __global__ void __launch_bounds__(256, PREC == kF16 && MF <= 8 ? 2 : 1)
-    gemm_xlds_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
+    gemm_xlds_kernel(GemmArgs a, int n_tiles, int m_tiles, int units) {
   constexpr int BM = 16 * MF, BN = 64 * NFW, NT = 256;
   constexpr bool kLoA = PREC >= kSplitA, kLoB = PREC == kSplitAB;
   constexpr int XP = kLoA ? 2 : 1;                  // activation parts (hi, lo)
@@ -277,13 +292,9 @@ __global__ void __launch_bounds__(256, PREC == kF16 && MF <= 8 ? 2 : 1)
   extern __shared__ float lds[];
   half8* xs = reinterpret_cast<half8*>(lds);        // [2][XP][MF][KC][64]
   const int M = a.device_m ? *a.device_m : a.M;
-  const int slots = n_groups * m_tiles * 8;
-  const int split = blockIdx.x / slots;
-  const int r = blockIdx.x - split * slots;
-  const int group_m = r >> 3;
-  const int group = group_m / m_tiles, tile_m = group_m - group * m_tiles;
-  const int tile_n = group * 8 + (r & 7);
-  if (tile_n >= n_tiles || tile_m * BM >= M) return;  // uniform over the workgroup
+  const TileCoord at = xcd_tile(blockIdx.x, n_tiles, m_tiles, units);
+  const int split = at.split, tile_n = at.tile_n, tile_m = at.tile_m;
+  if (!at.valid || tile_m * BM >= M) return;  // uniform over the workgroup
   const int tile = tile_m * n_tiles + tile_n;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int KT = (int)(a.Kp >> 5);
@@ -620,7 +631,7 @@ struct Ring {
 
 template <int BM, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
-    gemm_dma_kernel(GemmArgs a, int n_tiles, int m_tiles, int n_groups) {
+    gemm_dma_kernel(GemmArgs a, int n_tiles, int m_tiles, int units) {
   using namespace dma;
   using R = Ring<BM>;
   constexpr int NS = R::kBuffers;
@@ -632,13 +643,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
   extern __shared__ float lds[];
   const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
   const int M = a.device_m ? *a.device_m : a.M;
-  const int slots = n_groups * m_tiles * 8;
-  const int split = blockIdx.x / slots;
-  const int r = blockIdx.x - split * slots;
-  const int group_m = r >> 3;
-  const int group = group_m / m_tiles, tile_m = group_m - group * m_tiles;
-  const int tile_n = group * 8 + (r & 7);
-  if (tile_n >= n_tiles || tile_m * BM >= M) return;  // uniform over the workgroup
+  const TileCoord at = xcd_tile(blockIdx.x, n_tiles, m_tiles, units);
+  const int split = at.split, tile_n = at.tile_n, tile_m = at.tile_m;
+  if (!at.valid || tile_m * BM >= M) return;  // uniform over the workgroup
   const int tile = tile_m * n_tiles + tile_n;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -906,7 +913,6 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
   constexpr int BM = 16 * MF, BN = 64 * NFW;
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
-  const int n_groups = (n_tiles + kXcds - 1) / kXcds;
   const int tiles = n_tiles * m_tiles;
   const int KT = (int)(a.Kp >> 5);
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
@@ -917,7 +923,8 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
   a.ksplit = ksplit;
   const int xp = prec >= kSplitA ? 2 : 1;
   const size_t lds = (size_t)2 * MF * KC * 64 * xp * 16;
-  dim3 grid((unsigned)(ksplit * n_groups * m_tiles * kXcds));
+  const int units = ksplit * n_tiles;
+  dim3 grid(xcd_grid(units, m_tiles));
   auto go = [&](auto kernel, const char* name) {
     static const bool configured = [kernel] {
       HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -925,7 +932,7 @@ int launch_xlds(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int ta
       return true;
     }();
     (void)configured;
-    observed(name, [&] { kernel<<<grid, 256, lds, stream>>>(a, n_tiles, m_tiles, n_groups); });
+    observed(name, [&] { kernel<<<grid, 256, lds, stream>>>(a, n_tiles, m_tiles, units); });
   };
   if constexpr (MF > 8) {
     go(&gemm_xlds_kernel<MF, NFW, KC, P, kF16>, kernel_name<MF, NFW, KC, P, kF16>("gemm_xlds_kernel"));
@@ -957,7 +964,6 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
   if (prec != kF16) return launch_xlds<8, 4, 4, 2>(stream, a, prec, rows_bound, target_ctas, forced_ksplit);
   const int n_tiles = (a.N + BN - 1) / BN;
   const int m_tiles = (rows_bound + BM - 1) / BM;
-  const int n_groups = (n_tiles + kXcds - 1) / kXcds;
   const int tiles = n_tiles * m_tiles;
   const int KT = (int)(a.Kp >> 5);
   if ((uint64_t)n_tiles * BN > a.w_rows_padded) fail(HLLM_INTERNAL, "GEMM tile exceeds the weight padding");
@@ -972,9 +978,10 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
     return true;
   }();
   (void)configured;
-  const dim3 grid((unsigned)(ksplit * n_groups * m_tiles * kXcds));
+  const int units = ksplit * n_tiles;
+  const dim3 grid(xcd_grid(units, m_tiles));
   observed(kernel_name<BM, WM, WN>("gemm_dma_kernel"), [&] {
-    gemm_dma_kernel<BM, WM, WN><<<grid, 64 * WM * WN, R::kLds, stream>>>(a, n_tiles, m_tiles, n_groups);
+    gemm_dma_kernel<BM, WM, WN><<<grid, 64 * WM * WN, R::kLds, stream>>>(a, n_tiles, m_tiles, units);
   });
   if (ksplit > 1 && a.defer_reduce) return ksplit;
   if (ksplit > 1) {
@@ -1237,14 +1244,23 @@ struct Choice {
 //    in LDS once per 256-feature tile wins;
 //  - more rows: the activation-staged kernel, BM 64, or BM 128 from 384 rows; wide outputs
 //    from 192 to 768 rows use the kernels that copy both operands to LDS (BM 128 below
-//    448 rows, BM 256 from there), and BM 128 activation-staged tiles beyond.
+//    448 rows, BM 256 from there), and BM 128 activation-staged tiles beyond; so do the
+//    deferred projections of chunk-sized F16 passes (BM 128, fewer K splits than the
+//    activation-staged kernel needs, so their consumers also read fewer partials).
 // K is split while there are few output tiles. When the consumer sums the partials
 // (`deferred`) a split costs one partial write, so about 220-280 workgroups are targeted;
 // otherwise a reduce kernel reads every partial back, so splits stop at about 200
 // workgroups, in powers of two.
-Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred) {
+Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16) {
   const bool wide = n >= 16384;
   const auto rounded = [](double x) { return std::max(1, (int)(x + 0.5)); };
+  if (f16 && deferred && rows <= 768 && (rows >= 448 || (n >= 4096 && rows >= 384))) {
+    // Deferred projections of chunk-sized passes (q/k/v from 384 rows, o and down from
+    // 448): both operands copied to LDS in 128 x 256 tiles, about 200 workgroups, at least
+    // two K splits.
+    const long tiles = (long)((n + 255) / 256) * ((rows + 127) / 128);
+    return {15, std::min(std::max(rounded(200.0 / (double)tiles), 2), 8)};
+  }
   if (rows <= 64 && (!wide || rows <= 32)) {
     const int config = rows <= 16 ? 0 : rows <= 32 ? 1 : 2;
     const int tiles = (n + 63) / 64;
@@ -1366,7 +1382,7 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
     return launch_decode(stream, args, rows_bound, cus);
   if (forced == kDecodeConfig && prec == kF16 && rows_bound <= 64 && (args.defer_reduce || args.epilogue == kEpiSwiglu))
     return launch_decode(stream, args, rows_bound, cus);
-  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0);
+  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0, prec == kF16);
   if (forced >= 0 && forced != kDecodeConfig) c = {forced, 0};
   return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }
