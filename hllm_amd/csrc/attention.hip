@@ -57,6 +57,103 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 
 // ---------------------------------------------------------------- MFMA flash attention
 
+// LDS of the MFMA kernel: the split-key merge uses [128 + 4 * D * 16] floats; fused decode
+// rows stage after it their query vectors [16][D] F32, the row's own key and value [2][D]
+// F16 and the own-key scores [16].
+template <int D>
+constexpr int kFusedBase = 128 + 4 * D * 16;
+
+// Fused decode rows (AttentionRope), D = 128: lane l holds elements l and l + 64, the two
+// halves of a rotate-half pair. Each of the item's G query heads (and, for the item holding
+// the row's own position, its key and value) is computed in the order of
+// qkv_rope_append_kernel: the projection's K-split partials summed in split order from
+// zero, QK-norm v * (inv * w), then RoPE; the key and value are rounded to F16, appended to
+// the cache at the row's slot and staged. The query vectors are staged in F32, and the own
+// key's score of every vector (the F16 scaled query times the F16 key, summed in F32) too.
+// Called by every thread of the workgroup (it holds the workgroup's barriers).
+template <int D>
+__device__ void fused_projection(const AttentionArgs& a, const AttnWork& w, int kvh, int G, int wave, int lane,
+                                 bool holds_self, float qscale) {
+  extern __shared__ float smem[];
+  float* qs = smem + kFusedBase<D>;
+  _Float16* self_kv = reinterpret_cast<_Float16*>(qs + 16 * D);
+  float* self_s = qs + 16 * D + D;
+  const AttentionRope& rp = a.rope;
+  const int heads = a.q_heads + 2 * a.kv_heads;
+  const size_t row_at = (size_t)w.row0 * heads * D;
+  const int jobs = G + (holds_self ? 2 : 0);
+  for (int job = wave; job < jobs; job += kThreads / 64) {  // wave-uniform
+    const bool is_q = job < G, is_v = job == G + 1;
+    const int head = is_q ? kvh * G + job : a.q_heads + (is_v ? a.kv_heads : 0) + kvh;
+    const size_t at = row_at + (size_t)head * D + lane;
+    float x[2] = {0.0f, 0.0f};
+    if (rp.parts.parts > 0) {
+      for (int s0 = 0; s0 < rp.parts.parts; s0 += 4) {
+        float p[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            p[u][j] = rp.parts.data[(size_t)min(s0 + u, rp.parts.parts - 1) * rp.parts.stride + at + 64 * j];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) x[j] = s0 + u < rp.parts.parts ? x[j] + p[u][j] : x[j];
+      }
+    } else {
+      x[0] = rp.qkv[at];
+      x[1] = rp.qkv[at + 64];
+    }
+    if (!is_v) {
+      float squares = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) squares += x[j] * x[j];
+      const float* nw = is_q ? rp.q_norm : rp.k_norm;
+      if (nw) {
+        squares = wave_sum(squares);
+        const float inverse = 1.0f / sqrtf(squares / (float)D + rp.eps);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) x[j] = x[j] * (inverse * nw[lane + 64 * j]);
+      }
+      const float c = rp.rope_cos[(size_t)w.position0 * (D / 2) + lane];
+      const float sn = rp.rope_sin[(size_t)w.position0 * (D / 2) + lane];
+      const float x0 = x[0], x1 = x[1];
+      x[0] = x0 * c - x1 * sn;
+      x[1] = x1 * c + x0 * sn;
+    }
+    if (is_q) {
+      qs[job * D + lane] = x[0];
+      qs[job * D + lane + 64] = x[1];
+    } else {
+      const int which = is_v ? 1 : 0;
+      const int slot = rp.row_slot[w.row0];
+      const int block = slot / a.kv.block_tokens, offset = slot - block * a.kv.block_tokens;
+      _Float16* pool = static_cast<_Float16*>(a.kv.pool);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d = lane + 64 * j;
+        const _Float16 h = to_half(x[j]);
+        self_kv[which * D + d] = h;
+        pool[which ? kv_value_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)
+                   : kv_key_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)] = h;
+      }
+    }
+  }
+  __syncthreads();
+  if (!holds_self) return;
+  for (int g = wave; g < G; g += kThreads / 64) {
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int d = lane + 64 * j;
+      part += (float)to_half(qs[g * D + d] * qscale) * (float)self_kv[d];
+    }
+    part = wave_sum(part);
+    if (lane == 0) self_s[g] = part;
+  }
+  __syncthreads();
+}
+
 // Three workgroups per CU for D <= 128: decode-like blocks hold one K/V tile per wave at a
 // time (registers for a second one would allow only two), so that more work items are in
 // flight for about the same bytes in flight.
@@ -95,11 +192,28 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     return (uint64_t)(uint32_t)table[__builtin_amdgcn_readfirstlane(logical)];
   };
   const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
+  // Fused decode rows (AttentionRope): the item holding the row's own position takes that
+  // key from registers, so its tiles end one position earlier.
+  const bool fused = D == 128 && a.rope.qkv != nullptr;
+  const bool holds_self = fused && w.key_end == w.position0 + 1;
+  const int key_end = holds_self ? w.key_end - 1 : w.key_end;
+  float* self_s = smem + kFusedBase<D> + 16 * D + D;  // fused: [16] own-key scores
+  const _Float16* self_kv = reinterpret_cast<const _Float16*>(smem + kFusedBase<D> + 16 * D);  // fused: [2][D]
 
   // Q^T as the B operand (1/sqrt(D) and log2 e folded in): lane holds Q[v][32 kk + 8 quad + j].
   const float qscale = a.scale * kLog2e;
   half8 qf[KK];
-  {
+  if constexpr (D == 128) {
+    if (fused) fused_projection<D>(a, w, kvh, G, wave, lane, holds_self, qscale);
+  }
+  if (fused) {
+    // The scaled vectors staged by fused_projection.
+    const float* qrow = smem + kFusedBase<D> + (v_ok ? vg : 0) * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[kk][j] = v_ok ? to_half(qrow[32 * kk + 8 * quad + j] * qscale) : (_Float16)0.0f;
+  } else {
     const float* qrow = a.q + ((size_t)(w.row0 + (v_ok ? vr : 0)) * a.q_heads + kvh * G + vg) * D;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
@@ -153,7 +267,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   // no mask (the usual case). Vectors past the block's end are not masked: their results
   // are never written.
   float sc[8];
-  if (t + 32 <= w.key_end && t + 31 <= w.position0) {
+  if (t + 32 <= key_end && t + 31 <= w.position0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       sc[i] = s0[i];
@@ -163,8 +277,8 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p0 = t + 8 * quad + i, p1 = t + 8 * quad + 4 + i;
-      sc[i] = (p0 <= my_pos && p0 < w.key_end) ? s0[i] : -INFINITY;
-      sc[4 + i] = (p1 <= my_pos && p1 < w.key_end) ? s1[i] : -INFINITY;
+      sc[i] = (p0 <= my_pos && p0 < key_end) ? s0[i] : -INFINITY;
+      sc[4 + i] = (p1 <= my_pos && p1 < key_end) ? s1[i] : -INFINITY;
     }
   }
   float tmax = sc[0];
@@ -189,7 +303,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   m = m_new;
   // A tile that runs past the key range reads cache slots no pass has written: zero
   // them, since a zero probability does not cancel a non-finite value.
-  const bool tail = t + 32 > w.key_end;
+  const bool tail = t + 32 > key_end;
 #pragma unroll
   for (int df = 0; df < DF; ++df) {
     o[df][0] *= alpha;
@@ -200,7 +314,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     if (tail) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (t + 8 * quad + j >= w.key_end) av[j] = (_Float16)0.0f;
+        if (t + 8 * quad + j >= key_end) av[j] = (_Float16)0.0f;
     }
     o[df] = mfma(av, pf, o[df]);
   }
@@ -211,16 +325,33 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     // fragments from HBM straight into registers, one tile per wave at a time (the other
     // workgroups on the CU keep the memory busy meanwhile). The next tile's block is read
     // one iteration early; past the range it re-reads the range's last tile's block.
-    const int last_tile = w.key_begin + ((w.key_end - 1 - w.key_begin) & ~31);
-    auto clamp_tile = [&](int x) { return x < w.key_end ? x : last_tile; };
-    constexpr int stride = 4;
-    int t = w.key_begin + 32 * wave;
-    uint64_t blk = block_of(clamp_tile(t) / bt);
-    for (; t < w.key_end; t += 32 * stride) {
-      Tile cur;
-      fetch(t, blk, cur);
-      blk = block_of(clamp_tile(t + 32 * stride) / bt);
-      consume(t, cur);
+    if (key_end > w.key_begin) {  // a fused row's first position has no cached keys
+      const int last_tile = w.key_begin + ((key_end - 1 - w.key_begin) & ~31);
+      auto clamp_tile = [&](int x) { return x < key_end ? x : last_tile; };
+      constexpr int stride = 4;
+      int t = w.key_begin + 32 * wave;
+      uint64_t blk = block_of(clamp_tile(t) / bt);
+      for (; t < key_end; t += 32 * stride) {
+        Tile cur;
+        fetch(t, blk, cur);
+        blk = block_of(clamp_tile(t + 32 * stride) / bt);
+        consume(t, cur);
+      }
+    }
+    if (holds_self && wave == 0 && v_ok) {
+      // The row's own key and value (staged by fused_projection), one more softmax step:
+      // the probability enters the sum in F32 and the value product in F16, as in a tile.
+      const float sv = self_s[vg];
+      const float m_new = fmaxf(m, sv);
+      const float alpha = exp2_fast(m - m_new);
+      const float p = exp2_fast(sv - m_new);
+      l = l * alpha + p;
+      m = m_new;
+      const float p16 = (float)to_half(p);
+#pragma unroll
+      for (int df = 0; df < DF; ++df)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[df][i] = o[df][i] * alpha + p16 * (float)self_kv[D + 16 * df + 4 * quad + i];
     }
   } else {
     // Prefill blocks: every wave needs every tile, so the workgroup copies each 32-key K/V

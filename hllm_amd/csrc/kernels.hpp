@@ -173,6 +173,23 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
 
 // Split-context GQA attention for every packed row against its sequence's paged cache
 // (positions 0..row_position), then the split combine into F-layout A operands.
+// Decode rows with the projection epilogue fused into attention (F16 KV, head dim 128, passes
+// of single-token items): each item reads its row's q/k/v from the q/k/v projection output
+// (`qkv` [rows][(Q + 2K) * D], or its K-split partials), applies QK-norm and RoPE itself, and
+// the item that holds the row's own position appends the row's K/V to the cache and adds the
+// row's own key to the softmax from registers. qkv == nullptr: q comes from `q`, K/V are in
+// the cache already.
+struct AttentionRope {
+  const float* qkv = nullptr;
+  Partials parts;
+  const float* q_norm = nullptr;  // nullptr: no QK-norm
+  const float* k_norm = nullptr;
+  float eps = 0.0f;
+  const float* rope_cos = nullptr;  // [positions][D / 2]
+  const float* rope_sin = nullptr;
+  const int32_t* row_slot = nullptr;
+};
+
 struct AttentionArgs {
   const float* q;              // [rows][Q][D]
   int rows, q_heads, kv_heads, head_dim;
@@ -195,6 +212,7 @@ struct AttentionArgs {
   uint16_t* out_hi;            // F-layout [rows][Q * D]
   uint16_t* out_lo;
   uint64_t out_cols_padded;
+  AttentionRope rope;
 };
 void launch_attention(hipStream_t stream, const AttentionArgs& a);
 // Whether launch_attention uses the MFMA kernel (and hence the pack kernel's work list).

@@ -207,15 +207,17 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[q][j] = 0.0f;
       const float* base = residual.data + (size_t)src * hidden;
-      for (int s0 = 0; s0 < residual.parts; s0 += 4) {
-        float p[4][Q][8];
+      // Up to eight splits' loads in flight at once (four when a thread holds two chunks).
+      constexpr int U = Q == 1 ? 8 : 4;
+      for (int s0 = 0; s0 < residual.parts; s0 += U) {
+        float p[U][Q][8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int q = 0; q < Q; ++q)
             load8_at(base + (size_t)min(s0 + u, residual.parts - 1) * residual.stride + c[q], p[u][q]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int q = 0; q < Q; ++q)
 #pragma unroll

@@ -24,6 +24,16 @@ thread_local std::string g_last_error;
 
 uint64_t pad_to(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
 
+// Decode passes fuse QK-norm, RoPE and the K/V append into attention unless
+// HLLM_ROCM_ROPE_FUSION=0 (the separate kernel, for comparisons).
+bool rope_fusion_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("HLLM_ROCM_ROPE_FUSION");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 // Device allocation owned by the stage (RAII: a failed construction frees what it got).
 struct DeviceMemory {
   void* ptr = nullptr;
@@ -1152,6 +1162,10 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
     }
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
+  // Passes of single-token items (decode rows) at head dim 128 with F16 KV: QK-norm, RoPE and
+  // the K/V append run inside the attention kernel (AttentionRope), one launch fewer per layer.
+  bool fuse_rope = mfma_attention_ && !kv_f32_ && D_ == 128 && Q_ / K_ <= 16 && rope_fusion_enabled();
+  for (uint32_t i = 0; i < n && fuse_rope; ++i) fuse_rope = pass.item[i].query_tokens == 1;
 
   // ---- device work. Every launch parameter below is a function of the pass shape (n, R,
   // S, sampler): the rest is read on the device. `capturing`: recorded into a graph.
@@ -1203,14 +1217,26 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
       pending = {};
       const int qkv_parts = gemm("gemm_qkv", w.qkv, a0h, a0l, R, (int)qkv_n_, kEpiStore, qkv_.as<float>(),
                                  (int)qkv_n_, nullptr, nullptr, 0, true);
-      timed("rope_append", (uint64_t)R * qkv_n_ * 6, 0.0, [&] {
-        launch_qkv_rope_append(stream_, qkv_.as<float>(), R, (int)Q_, (int)K_, (int)D_,
-                               c_.query_key_norm ? w.q_norm.as<float>() : nullptr,
-                               c_.query_key_norm ? w.k_norm.as<float>() : nullptr, eps, rope_cos_.as<float>(),
-                               rope_sin_.as<float>(), pack_.row_position, pack_.row_slot, kv_, (int)l,
-                               q_.as<float>(), Partials{ws, qkv_parts, (uint64_t)R * qkv_n_});
-      });
+      if (!fuse_rope) {
+        timed("rope_append", (uint64_t)R * qkv_n_ * 6, 0.0, [&] {
+          launch_qkv_rope_append(stream_, qkv_.as<float>(), R, (int)Q_, (int)K_, (int)D_,
+                                 c_.query_key_norm ? w.q_norm.as<float>() : nullptr,
+                                 c_.query_key_norm ? w.k_norm.as<float>() : nullptr, eps, rope_cos_.as<float>(),
+                                 rope_sin_.as<float>(), pack_.row_position, pack_.row_slot, kv_, (int)l,
+                                 q_.as<float>(), Partials{ws, qkv_parts, (uint64_t)R * qkv_n_});
+        });
+      }
       AttentionArgs at{};
+      if (fuse_rope) {
+        at.rope.qkv = qkv_.as<float>();
+        at.rope.parts = Partials{ws, qkv_parts, (uint64_t)R * qkv_n_};
+        at.rope.q_norm = c_.query_key_norm ? w.q_norm.as<float>() : nullptr;
+        at.rope.k_norm = c_.query_key_norm ? w.k_norm.as<float>() : nullptr;
+        at.rope.eps = eps;
+        at.rope.rope_cos = rope_cos_.as<float>();
+        at.rope.rope_sin = rope_sin_.as<float>();
+        at.rope.row_slot = pack_.row_slot;
+      }
       at.work = attn_work_.as<AttnWork>();
       at.work_count = attn_count_.as<int32_t>();
       at.work_grid = attn_grid;
