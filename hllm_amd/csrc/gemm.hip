@@ -1251,15 +1251,17 @@ struct Choice {
 // (`deferred`) a split costs one partial write, so about 220-280 workgroups are targeted;
 // otherwise a reduce kernel reads every partial back, so splits stop at about 200
 // workgroups, in powers of two.
-Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16) {
+Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cus) {
   const bool wide = n >= 16384;
   const auto rounded = [](double x) { return std::max(1, (int)(x + 0.5)); };
   if (f16 && deferred && rows <= 768 && (rows >= 448 || (n >= 4096 && rows >= 384))) {
     // Deferred projections of chunk-sized passes (q/k/v from 384 rows, o and down from
-    // 448): both operands copied to LDS in 128 x 256 tiles, about 200 workgroups, at least
-    // two K splits.
-    const long tiles = (long)((n + 255) / 256) * ((rows + 127) / 128);
-    return {15, std::min(std::max(rounded(200.0 / (double)tiles), 2), 8)};
+    // 448): both operands copied to LDS in 128 x 256 tiles (one workgroup per CU), with the
+    // most K splits (2 to 8) whose workgroups fit every XCD's CUs at once (xcd_tile).
+    const int n_tiles = (n + 255) / 256, m_tiles = (rows + 127) / 128, per_xcd = std::max(1, cus / kXcds);
+    int ks = 8;
+    while (ks > 2 && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
+    return {15, ks};
   }
   if (rows <= 64 && (!wide || rows <= 32)) {
     const int config = rows <= 16 ? 0 : rows <= 32 ? 1 : 2;
@@ -1382,7 +1384,7 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
     return launch_decode(stream, args, rows_bound, cus);
   if (forced == kDecodeConfig && prec == kF16 && rows_bound <= 64 && (args.defer_reduce || args.epilogue == kEpiSwiglu))
     return launch_decode(stream, args, rows_bound, cus);
-  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0, prec == kF16);
+  Choice c = gemm_choice(rows_bound, args.N, args.Kp, args.defer_reduce != 0, prec == kF16, cus);
   if (forced >= 0 && forced != kDecodeConfig) c = {forced, 0};
   return launch_gemm_config(stream, args, prec, rows_bound, cus, c.config, c.ksplit);
 }
