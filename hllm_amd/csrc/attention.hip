@@ -58,8 +58,8 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 // ---------------------------------------------------------------- MFMA flash attention
 
 // LDS of the MFMA kernel: the split-key merge uses [128 + 4 * D * 16] floats; fused decode
-// rows stage after it their query vectors [16][D] F32, the row's own key and value [2][D]
-// F16 and the own-key scores [16].
+// rows stage after it their query vectors [16][D] F32 and the row's own key and value
+// [2][D] F16.
 template <int D>
 constexpr int kFusedBase = 128 + 4 * D * 16;
 
@@ -68,16 +68,14 @@ constexpr int kFusedBase = 128 + 4 * D * 16;
 // the row's own position, its key and value) is computed in the order of
 // qkv_rope_append_kernel: the projection's K-split partials summed in split order from
 // zero, QK-norm v * (inv * w), then RoPE; the key and value are rounded to F16, appended to
-// the cache at the row's slot and staged. The query vectors are staged in F32, and the own
-// key's score of every vector (the F16 scaled query times the F16 key, summed in F32) too.
-// Called by every thread of the workgroup (it holds the workgroup's barriers).
+// the cache at the row's slot and staged; the query vectors are staged in F32. Called by
+// every thread of the workgroup (it holds the workgroup's barrier).
 template <int D>
 __device__ void fused_projection(const AttentionArgs& a, const AttnWork& w, int kvh, int G, int wave, int lane,
-                                 bool holds_self, float qscale) {
+                                 bool holds_self) {
   extern __shared__ float smem[];
   float* qs = smem + kFusedBase<D>;
   _Float16* self_kv = reinterpret_cast<_Float16*>(qs + 16 * D);
-  float* self_s = qs + 16 * D + D;
   const AttentionRope& rp = a.rope;
   const int heads = a.q_heads + 2 * a.kv_heads;
   const size_t row_at = (size_t)w.row0 * heads * D;
@@ -140,18 +138,22 @@ __device__ void fused_projection(const AttentionArgs& a, const AttnWork& w, int 
     }
   }
   __syncthreads();
-  if (!holds_self) return;
-  for (int g = wave; g < G; g += kThreads / 64) {
-    float part = 0.0f;
+}
+
+// The own-key score of vector g of a fused item (the F16 scaled query times the F16 key,
+// summed in F32), from the vectors and key staged by fused_projection; called by a whole wave.
+template <int D>
+__device__ float own_key_score(int g, int lane, float qscale) {
+  extern __shared__ float smem[];
+  const float* qs = smem + kFusedBase<D>;
+  const _Float16* self_kv = reinterpret_cast<const _Float16*>(qs + 16 * D);
+  float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int d = lane + 64 * j;
-      part += (float)to_half(qs[g * D + d] * qscale) * (float)self_kv[d];
-    }
-    part = wave_sum(part);
-    if (lane == 0) self_s[g] = part;
+  for (int j = 0; j < 2; ++j) {
+    const int d = lane + 64 * j;
+    part += (float)to_half(qs[g * D + d] * qscale) * (float)self_kv[d];
   }
-  __syncthreads();
+  return wave_sum(part);
 }
 
 // Three workgroups per CU for D <= 128: decode-like blocks hold one K/V tile per wave at a
@@ -197,14 +199,13 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   const bool fused = D == 128 && a.rope.qkv != nullptr;
   const bool holds_self = fused && w.key_end == w.position0 + 1;
   const int key_end = holds_self ? w.key_end - 1 : w.key_end;
-  float* self_s = smem + kFusedBase<D> + 16 * D + D;  // fused: [16] own-key scores
   const _Float16* self_kv = reinterpret_cast<const _Float16*>(smem + kFusedBase<D> + 16 * D);  // fused: [2][D]
 
   // Q^T as the B operand (1/sqrt(D) and log2 e folded in): lane holds Q[v][32 kk + 8 quad + j].
   const float qscale = a.scale * kLog2e;
   half8 qf[KK];
   if constexpr (D == 128) {
-    if (fused) fused_projection<D>(a, w, kvh, G, wave, lane, holds_self, qscale);
+    if (fused) fused_projection<D>(a, w, kvh, G, wave, lane, holds_self);
   }
   if (fused) {
     // The scaled vectors staged by fused_projection.
@@ -338,10 +339,18 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
         consume(t, cur);
       }
     }
+    float own = 0.0f;  // wave 0: the own-key score of this lane's vector (all vectors in turn)
+    if constexpr (D == 128) {
+      if (holds_self && wave == 0)
+        for (int g = 0; g < G; ++g) {
+          const float sg = own_key_score<D>(g, lane, qscale);
+          if (g == vg) own = sg;
+        }
+    }
     if (holds_self && wave == 0 && v_ok) {
       // The row's own key and value (staged by fused_projection), one more softmax step:
       // the probability enters the sum in F32 and the value product in F16, as in a tile.
-      const float sv = self_s[vg];
+      const float sv = own;
       const float m_new = fmaxf(m, sv);
       const float alpha = exp2_fast(m - m_new);
       const float p = exp2_fast(sv - m_new);
