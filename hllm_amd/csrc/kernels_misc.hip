@@ -207,8 +207,8 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[q][j] = 0.0f;
       const float* base = residual.data + (size_t)src * hidden;
-      // Up to eight splits' loads in flight at once (four when a thread holds two chunks).
-      constexpr int U = Q == 1 ? 8 : 4;
+      // Up to sixteen splits' loads in flight at once (four when a thread holds two chunks).
+      constexpr int U = Q == 1 ? 16 : 4;
       for (int s0 = 0; s0 < residual.parts; s0 += U) {
         float p[U][Q][8];
 #pragma unroll
