@@ -60,6 +60,14 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 // LDS of the MFMA kernel: the split-key merge uses [128 + 4 * D * 16] floats; fused decode
 // rows stage after it their query vectors [16][D] F32 and the row's own key and value
 // [2][D] F16.
+// A load of a workgroup-uniform address from memory no kernel of the launch writes (the
+// work list, items, block table, row slots): through the constant address space, so that the
+// compiler issues it as a scalar load.
+template <typename T>
+__device__ inline T uniform_load(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
 template <int D>
 constexpr int kFusedBase = 128 + 4 * D * 16;
 
@@ -68,72 +76,113 @@ constexpr int kFusedBase = 128 + 4 * D * 16;
 // the row's own position, its key and value) is computed in the order of
 // qkv_rope_append_kernel: the projection's K-split partials summed in split order from
 // zero, QK-norm v * (inv * w), then RoPE; the key and value are rounded to F16, appended to
-// the cache at the row's slot and staged; the query vectors are staged in F32. Called by
-// every thread of the workgroup (it holds the workgroup's barrier).
+// the cache at the row's slot and staged; the query vectors are staged in F32. A wave takes
+// its jobs two at a time and issues every load of both (the first four partial splits, the
+// norm weights, the RoPE factors and the slot) before any arithmetic: the phase is one memory
+// round trip per pair instead of three per job. Called by every thread of the workgroup (it
+// holds the workgroup's barrier).
 template <int D>
 __device__ void fused_projection(const AttentionArgs& a, const AttnWork& w, int kvh, int G, int wave, int lane,
                                  bool holds_self) {
   extern __shared__ float smem[];
+  constexpr int kWaves = kThreads / 64;
   float* qs = smem + kFusedBase<D>;
   _Float16* self_kv = reinterpret_cast<_Float16*>(qs + 16 * D);
   const AttentionRope& rp = a.rope;
   const int heads = a.q_heads + 2 * a.kv_heads;
   const size_t row_at = (size_t)w.row0 * heads * D;
   const int jobs = G + (holds_self ? 2 : 0);
-  for (int job = wave; job < jobs; job += kThreads / 64) {  // wave-uniform
-    const bool is_q = job < G, is_v = job == G + 1;
-    const int head = is_q ? kvh * G + job : a.q_heads + (is_v ? a.kv_heads : 0) + kvh;
-    const size_t at = row_at + (size_t)head * D + lane;
-    float x[2] = {0.0f, 0.0f};
-    if (rp.parts.parts > 0) {
-      for (int s0 = 0; s0 < rp.parts.parts; s0 += 4) {
-        float p[4][2];
+  const int parts = rp.parts.parts;
+  const float c = rp.rope_cos[(size_t)w.position0 * (D / 2) + lane];
+  const float sn = rp.rope_sin[(size_t)w.position0 * (D / 2) + lane];
+  const int slot = holds_self ? uniform_load(rp.row_slot + w.row0) : 0;
+  for (int job0 = wave; job0 < jobs; job0 += 2 * kWaves) {  // wave-uniform
+    // Job k of the pair is job0 + k * kWaves; a second job past the last one repeats the
+    // last one's loads and writes nothing.
+    int job[2];
+    bool is_q[2], is_v[2];
+    size_t at[2];
+    float p[2][4][2], nwv[2][2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      job[k] = min(job0 + k * kWaves, jobs - 1);
+      is_q[k] = job[k] < G;
+      is_v[k] = job[k] == G + 1;
+      const int head = is_q[k] ? kvh * G + job[k] : a.q_heads + (is_v[k] ? a.kv_heads : 0) + kvh;
+      at[k] = row_at + (size_t)head * D + lane;
+      if (parts > 0) {
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            p[u][j] = rp.parts.data[(size_t)min(s0 + u, rp.parts.parts - 1) * rp.parts.stride + at + 64 * j];
+          for (int j = 0; j < 2; ++j) p[k][u][j] = rp.parts.data[(size_t)min(u, parts - 1) * rp.parts.stride + at[k] + 64 * j];
+      } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) x[j] = s0 + u < rp.parts.parts ? x[j] + p[u][j] : x[j];
+        for (int j = 0; j < 2; ++j) p[k][0][j] = rp.qkv[at[k] + 64 * j];
       }
-    } else {
-      x[0] = rp.qkv[at];
-      x[1] = rp.qkv[at + 64];
-    }
-    if (!is_v) {
-      float squares = 0.0f;
+      const float* nw = is_q[k] ? rp.q_norm : rp.k_norm;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) squares += x[j] * x[j];
-      const float* nw = is_q ? rp.q_norm : rp.k_norm;
-      if (nw) {
-        squares = wave_sum(squares);
-        const float inverse = 1.0f / sqrtf(squares / (float)D + rp.eps);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) x[j] = x[j] * (inverse * nw[lane + 64 * j]);
-      }
-      const float c = rp.rope_cos[(size_t)w.position0 * (D / 2) + lane];
-      const float sn = rp.rope_sin[(size_t)w.position0 * (D / 2) + lane];
-      const float x0 = x[0], x1 = x[1];
-      x[0] = x0 * c - x1 * sn;
-      x[1] = x1 * c + x0 * sn;
+      for (int j = 0; j < 2; ++j) nwv[k][j] = nw && !is_v[k] ? nw[lane + 64 * j] : 1.0f;
     }
-    if (is_q) {
-      qs[job * D + lane] = x[0];
-      qs[job * D + lane + 64] = x[1];
-    } else {
-      const int which = is_v ? 1 : 0;
-      const int slot = rp.row_slot[w.row0];
-      const int block = slot / a.kv.block_tokens, offset = slot - block * a.kv.block_tokens;
-      _Float16* pool = static_cast<_Float16*>(a.kv.pool);
+    float x[2][2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int d = lane + 64 * j;
-        const _Float16 h = to_half(x[j]);
-        self_kv[which * D + d] = h;
-        pool[which ? kv_value_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)
-                   : kv_key_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)] = h;
+        if (parts > 0) {
+          x[k][j] = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[k][j] = u < parts ? x[k][j] + p[k][u][j] : x[k][j];
+        } else {
+          x[k][j] = p[k][0][j];
+        }
+      }
+      for (int s0 = 4; s0 < parts; s0 += 4) {  // splits past the first four (none on most shapes)
+        float q[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) q[u][j] = rp.parts.data[(size_t)min(s0 + u, parts - 1) * rp.parts.stride + at[k] + 64 * j];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) x[k][j] = s0 + u < parts ? x[k][j] + q[u][j] : x[k][j];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (!is_v[k]) {
+        if (is_q[k] ? rp.q_norm : rp.k_norm) {
+          float squares = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) squares += x[k][j] * x[k][j];
+          squares = wave_sum(squares);
+          const float inverse = 1.0f / sqrtf(squares / (float)D + rp.eps);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) x[k][j] = x[k][j] * (inverse * nwv[k][j]);
+        }
+        const float x0 = x[k][0], x1 = x[k][1];
+        x[k][0] = x0 * c - x1 * sn;
+        x[k][1] = x1 * c + x0 * sn;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (job0 + k * kWaves >= jobs) continue;
+      if (is_q[k]) {
+        qs[job[k] * D + lane] = x[k][0];
+        qs[job[k] * D + lane + 64] = x[k][1];
+      } else {
+        const int which = is_v[k] ? 1 : 0;
+        const int block = slot / a.kv.block_tokens, offset = slot - block * a.kv.block_tokens;
+        _Float16* pool = static_cast<_Float16*>(a.kv.pool);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int d = lane + 64 * j;
+          const _Float16 h = to_half(x[k][j]);
+          self_kv[which * D + d] = h;
+          pool[which ? kv_value_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)
+                     : kv_key_index(a.kv, a.layer, (uint64_t)block, offset, kvh, d)] = h;
+        }
       }
     }
   }
@@ -167,11 +216,16 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   // Workgroups loop over (work item, KV head) pairs, KV heads innermost so that the
   // dispatch follows the list's order (the list's size is written by the pack kernel); a
   // launch may have fewer workgroups than pairs.
-  const int count = *a.work_count * a.kv_heads;
+  const int count = uniform_load(a.work_count) * a.kv_heads;
   for (int idx = blockIdx.x; idx < count; idx += gridDim.x) {
   [&] {
   const int wi = idx / a.kv_heads, kvh = idx - wi * a.kv_heads;
-  const AttnWork w = a.work[wi];
+  AttnWork w;
+  {
+    const int32_t* wp = reinterpret_cast<const int32_t*>(a.work + wi);
+    w = AttnWork{uniform_load(wp), uniform_load(wp + 1), uniform_load(wp + 2), uniform_load(wp + 3),
+                 uniform_load(wp + 4), uniform_load(wp + 5), uniform_load(wp + 6), uniform_load(wp + 7)};
+  }
   const int G = a.q_heads / a.kv_heads;
   const int nvec = w.rows * G;
   const bool split_keys = nvec <= 16;
@@ -182,7 +236,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   const bool v_ok = v < nvec;
   const int vr = v / G, vg = v - vr * G;
   const int my_pos = w.position0 + vr;
-  const int seq = a.items[w.item].sequence;
+  const int seq = uniform_load(&a.items[w.item].sequence);
   const int bt = a.kv.block_tokens, KVH = a.kv_heads;
   // Waves whose vectors lie past the block's end still stage K/V tiles and meet the
   // barriers of the prefill path; their results are never written.
@@ -191,7 +245,7 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
   // 32-key aligned and blocks a multiple of 32 keys, so a tile lies in one block.
   const int32_t* table = a.block_table + (size_t)seq * a.table_width;
   auto block_of = [&](int logical) -> uint64_t {
-    return (uint64_t)(uint32_t)table[__builtin_amdgcn_readfirstlane(logical)];
+    return (uint64_t)(uint32_t)uniform_load(table + __builtin_amdgcn_readfirstlane(logical));
   };
   const _Float16* pool = static_cast<const _Float16*>(a.kv.pool) + (uint64_t)a.layer * a.kv.layer_stride;
   // Fused decode rows (AttentionRope): the item holding the row's own position takes that
@@ -208,12 +262,20 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     if (fused) fused_projection<D>(a, w, kvh, G, wave, lane, holds_self);
   }
   if (fused) {
-    // The scaled vectors staged by fused_projection.
+    // The scaled vectors staged by fused_projection, read as 16-byte vectors whether or not
+    // the lane's vector exists (a conditional read per element would be 32 dependent LDS
+    // round trips).
     const float* qrow = smem + kFusedBase<D> + (v_ok ? vg : 0) * D;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
+    for (int kk = 0; kk < KK; ++kk) {
+      const floatx4 x0 = *reinterpret_cast<const floatx4*>(qrow + 32 * kk + 8 * quad);
+      const floatx4 x1 = *reinterpret_cast<const floatx4*>(qrow + 32 * kk + 8 * quad + 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qf[kk][j] = v_ok ? to_half(qrow[32 * kk + 8 * quad + j] * qscale) : (_Float16)0.0f;
+      for (int j = 0; j < 4; ++j) {
+        qf[kk][j] = v_ok ? to_half(x0[j] * qscale) : (_Float16)0.0f;
+        qf[kk][4 + j] = v_ok ? to_half(x1[j] * qscale) : (_Float16)0.0f;
+      }
+    }
   } else {
     const float* qrow = a.q + ((size_t)(w.row0 + (v_ok ? vr : 0)) * a.q_heads + kvh * G + vg) * D;
 #pragma unroll
@@ -464,18 +526,20 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
 
   float m_fin = m, l_fin = l;
   if (split_keys) {
-    // Merge the four waves' partial softmax states (vectors 0..15) through LDS.
-    float* sm_m = smem;            // [4][16]
-    float* sm_l = smem + 64;       // [4][16]
-    float* sm_o = smem + 128;      // [4][D][16]
+    // Merge the four waves' partial softmax states (vectors 0..15) through LDS. A lane's
+    // accumulators are stored lane-private, [wave][df][lane] x 4 floats, so that wave 0's
+    // lane reads the other waves' values of its own (vector, dimensions) as 16-byte vectors.
+    float* sm_m = smem;                                        // [4][16]
+    float* sm_l = smem + 64;                                   // [4][16]
+    floatx4* sm_o = reinterpret_cast<floatx4*>(smem + 128);    // [4][DF][64]
     if (quad == 0) {
       sm_m[wave * 16 + col] = m;
       sm_l[wave * 16 + col] = l;
     }
+    if (wave != 0) {
 #pragma unroll
-    for (int df = 0; df < DF; ++df)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm_o[(wave * D + 16 * df + 4 * quad + i) * 16 + col] = o[df][i];
+      for (int df = 0; df < DF; ++df) sm_o[(wave * DF + df) * 64 + lane] = o[df];
+    }
     __syncthreads();
     if (wave != 0) return;
     float mm = -INFINITY;
@@ -490,14 +554,18 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     }
     m_fin = mm;
 #pragma unroll
-    for (int df = 0; df < DF; ++df)
+    for (int df = 0; df < DF; ++df) {
+      floatx4 others[3];
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) others[ww - 1] = sm_o[(ww * DF + df) * 64 + lane];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float s = 0.0f;
+        float s = 0.0f + o[df][i] * weights[0];
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) s += sm_o[(ww * D + 16 * df + 4 * quad + i) * 16 + col] * weights[ww];
+        for (int ww = 1; ww < 4; ++ww) s += others[ww - 1][i] * weights[ww];
         o[df][i] = s;
       }
+    }
   }
   if (!v_ok) return;
   const int row = w.row0 + vr, qh = kvh * G + vg;
