@@ -1002,9 +1002,13 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
 // fragment (rows 4g + h and 4g + 2 + h of the interleaved gate/up matrix), so SwiGLU is
 // applied from the accumulators and no split-K reduction is ever needed for it. K is split
 // across workgroups only for deferred consumers (the K-split partials are summed in split
-// order by the kernel that reads the projection).
+// order by the kernel that reads the projection). With `whole` (deferred projections whose
+// split's activations fit in LDS), the split's activation fragments are copied into LDS once,
+// straight from memory (global_load_lds), before the loop: the activations of a decode pass
+// were just written by the previous kernel and miss in this XCD's L2, so one wait for all
+// of them replaces one per chunk, and the waves then run without per-chunk barriers.
 template <int MF, int WAVES, int NFW, int KC, int P, bool PAIR>
-__global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int n_tiles) {
+__global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int n_tiles, int whole) {
   constexpr int NT = 64 * WAVES, FR = WAVES * NFW;
   constexpr int CHUNK = MF * KC * 64;  // half8s per staged chunk
   constexpr int PIECES = (CHUNK + NT - 1) / NT;
@@ -1069,6 +1073,35 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
 #pragma unroll
     for (int j = 0; j < NFW; ++j) rb[slot][j] = __builtin_nontemporal_load(W[j] + (size_t)kt * 64);
   };
+  if (!PAIR && whole) {
+    // LDS holds fragment (i, s) of the split at (i * per + s) * 64 half8s.
+    const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+      for (int s = wave; s < steps; s += WAVES)  // wave-uniform
+        lds_copy16(X + (size_t)i * frag_stride + (size_t)(kt0 + s) * 64, (uint32_t)lane * 16,
+                   lds_base + (uint32_t)(i * per + s) * 1024);
+#pragma unroll
+    for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
+    wait_counts<0, 15>();
+    __syncthreads();
+    for (int s0 = 0; s0 < steps; s0 += P) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int step = s0 + j;
+        if (step < steps) {
+#pragma unroll
+          for (int i = 0; i < MF; ++i) {
+            const half8 x = xs[(i * per + step) * 64 + lane];
+#pragma unroll
+            for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[j][n], x, acc[i][n]);
+          }
+        }
+        load_w(j, kt0 + step + P);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
 #pragma unroll
   for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
   if (chunks > 0) {
@@ -1096,6 +1129,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
     }
     if (c + 1 < chunks) store_x((c + 1) & 1);
     __syncthreads();
+  }
   }
 
   // Lane (q = lane / 16, t = lane % 16) of accumulator (i, n) holds row 16 i + t, features
@@ -1144,6 +1178,12 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
   }
 }
 
+// LDS a decode workgroup may give to its split's whole activation range.
+constexpr size_t kDecodeWholeLds = 144 * 1024;
+namespace {
+int env_int(const char* name, int fallback);
+}  // namespace
+
 // Launches the decode kernel with `waves` waves per workgroup (4, 8 or 16) and the given
 // K split; returns the number of deferred partials (0: the epilogue has been applied).
 template <int MF, int NFW, int KC, int P, bool PAIR>
@@ -1155,7 +1195,12 @@ int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
   if (ksplit > 1 && (!a.defer_reduce || PAIR)) fail(HLLM_INTERNAL, "decode GEMM splits K only for deferred consumers");
   if (ksplit > 1 && (size_t)ksplit * a.M * a.N > a.workspace_floats) ksplit = 1;
   a.ksplit = ksplit;
-  const size_t lds = 2 * (size_t)MF * KC * 64 * 16;
+  // A deferred projection stages its split's activations whole when they fit in LDS.
+  const int KT = (int)(a.Kp >> 5);
+  const int per = ((KT + ksplit - 1) / ksplit + KC - 1) / KC * KC;
+  const size_t whole_lds = (size_t)MF * per * 1024;
+  const int whole = !PAIR && whole_lds <= kDecodeWholeLds && env_int("HLLM_ROCM_DECODE_WHOLE", 1) != 0;
+  const size_t lds = whole ? whole_lds : 2 * (size_t)MF * KC * 64 * 16;
   const dim3 grid((unsigned)(n_tiles * ksplit));
   auto go = [&](auto kernel, const char* name) {
     static const bool configured = [kernel] {
@@ -1164,7 +1209,7 @@ int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
       return true;
     }();
     (void)configured;
-    observed(name, [&] { kernel<<<grid, 64 * waves, lds, stream>>>(a, n_tiles); });
+    observed(name, [&] { kernel<<<grid, 64 * waves, lds, stream>>>(a, n_tiles, whole); });
   };
   if (waves >= 8)
     go(&gemm_decode_kernel<MF, 8, NFW, KC, P, PAIR>, kernel_name<MF, 8, NFW, KC, P, PAIR ? 1 : 0>("gemm_decode_kernel"));
