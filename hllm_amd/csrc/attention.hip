@@ -60,14 +60,6 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
 // LDS of the MFMA kernel: the split-key merge uses [128 + 4 * D * 16] floats; fused decode
 // rows stage after it their query vectors [16][D] F32 and the row's own key and value
 // [2][D] F16.
-// A load of a workgroup-uniform address from memory no kernel of the launch writes (the
-// work list, items, block table, row slots): through the constant address space, so that the
-// compiler issues it as a scalar load.
-template <typename T>
-__device__ inline T uniform_load(const T* p) {
-  return *(const __attribute__((address_space(4))) T*)(p);
-}
-
 template <int D>
 constexpr int kFusedBase = 128 + 4 * D * 16;
 
@@ -717,17 +709,17 @@ __global__ void __launch_bounds__(kThreads) attention_valu_kernel(AttentionArgs 
 // at clamped addresses): the kernel is a short latency-bound chain.
 template <int E>
 __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a, int mfma_path) {
-  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int pair = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (pair >= a.rows * a.q_heads) return;
   const int r = pair / a.q_heads, qh = pair - r * a.q_heads;
   const int D = a.head_dim;
   int splits;
   if (mfma_path) {
-    splits = a.row_splits[r];
+    splits = uniform_load(a.row_splits + r);
     if (splits == 1) return;
   } else {
-    const int ctx = a.row_position[r] + 1;
+    const int ctx = uniform_load(a.row_position + r) + 1;
     const int per = valu_split_length(ctx, a.max_splits, a.split_unit);
     splits = (ctx + per - 1) / per;
   }

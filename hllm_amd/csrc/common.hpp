@@ -108,6 +108,17 @@ __device__ inline float from_half_bits(uint16_t b) {
 //   3: split activations x split weights (F32 execution over F32-resident weights)
 enum Precision : int { kF16 = 1, kSplitA = 2, kSplitAB = 3 };
 
+// ------------------------------------------------------------ uniform loads
+
+// A load of a wave-uniform address from memory no kernel of the launch writes (work lists,
+// item tables, block tables, row maps, counts written by earlier launches): through the
+// constant address space, so that the compiler issues it as a scalar load instead of a vector
+// load it would have to wait for with the vector loads in flight.
+template <typename T>
+__device__ inline T uniform_load(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
 // ------------------------------------------------------------ direct copies to LDS
 
 // One 16-byte copy per lane from sbase + voffset to LDS byte m0 + 16 * lane; sbase and

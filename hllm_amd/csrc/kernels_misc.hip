@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* hi, const
                                                       const int32_t* row_token, int hidden,
                                                       float* h) {
   const int r = blockIdx.x;
-  const uint64_t id = (uint64_t)row_token[r];
+  const uint64_t id = (uint64_t)uniform_load(row_token + r);
   float* out = h + (size_t)r * hidden;
   for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
     const uint64_t at = flayout_index(id, c, cols_padded);
@@ -183,21 +183,25 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
     Partials residual) {
   __shared__ float scratch[16];
   const int r = blockIdx.x;
-  const int count = device_rows ? *device_rows : rows;
+  // The row count and the row map were written by earlier launches: scalar loads.
+  const int count = device_rows ? uniform_load(device_rows) : rows;
   if (r >= count) return;
-  const int src = row_index ? row_index[r] : r;
+  const int src = row_index ? uniform_load(row_index + r) : r;
   float* x = h + (size_t)src * hidden;
-  float v[Q][8];
+  float v[Q][8], wv[Q][8];
   int c0[Q];
 #pragma unroll
   for (int q = 0; q < Q; ++q) c0[q] = (threadIdx.x + q * blockDim.x) * 8;
   if ((hidden & 7) == 0) {
     int c[Q];  // clamped chunk columns
+    // The norm weights first (they do not depend on the row), then the row.
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
       c[q] = min(c0[q], hidden - 8);
-      load8_at(x + c[q], v[q]);
+      load8_at(weight + c[q], wv[q]);
     }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) load8_at(x + c[q], v[q]);
     if (residual.parts > 0) {
       // The projection's K-split partials summed in split order from zero, then the
       // residual add (the order of the reduce kernel's residual epilogue), written back.
@@ -242,6 +246,10 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
   } else {
     // Hidden sizes that are not a multiple of 8 (test models): element-wise.
 #pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wv[q][j] = c0[q] + j < hidden ? weight[c0[q] + j] : 0.0f;
+#pragma unroll
     for (int q = 0; q < Q; ++q) {
       load8(x, c0[q], hidden, false, v[q]);
       if (residual.parts > 0 && c0[q] < hidden) {
@@ -260,12 +268,6 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
       }
     }
   }
-  // The norm weights are loaded before the reduction, so their latency overlaps it.
-  float wv[Q][8];
-#pragma unroll
-  for (int q = 0; q < Q; ++q)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) wv[q][j] = c0[q] + j < hidden ? weight[c0[q] + j] : 0.0f;
   float squares = 0.0f;
 #pragma unroll
   for (int q = 0; q < Q; ++q)
