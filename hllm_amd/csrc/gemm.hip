@@ -637,9 +637,12 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
   constexpr int NS = R::kBuffers;
   constexpr int MF = BM / 16 / WM;                    // activation fragments per wave
   constexpr int NF = BN / 16 / WN;                    // weight fragments per wave
-  constexpr int kPer = R::kFrags / (WM * WN);         // copies per wave per k-step
+  // Copies per wave per k-step; when the waves do not divide the fragments, the extra copies
+  // repeat the last fragment (same source, same LDS bytes), so every wave issues the same
+  // number of copies per k-step and the in-flight counts below hold for all of them.
+  constexpr int kPer = (R::kFrags + WM * WN - 1) / (WM * WN);
   constexpr int kReads = MF + NF;                     // LDS reads per wave per k-step
-  static_assert(R::kFrags % (WM * WN) == 0 && NS >= 5 && kReads <= 15, "DMA GEMM shape");
+  static_assert(NS >= 5 && kReads <= 15, "DMA GEMM shape");
   extern __shared__ float lds[];
   const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
   const int M = a.device_m ? *a.device_m : a.M;
@@ -667,7 +670,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
     const size_t k = (size_t)min(kt0 + st, kt_last) * 1024;
 #pragma unroll
     for (int c = 0; c < kPer; ++c) {
-      const int f = wave * kPer + c;
+      const int f = min(wave * kPer + c, R::kFrags - 1);
       const char* src = f < BM / 16 ? X + (size_t)f * frag_stride * 16 : W + (size_t)(f - BM / 16) * frag_stride * 16;
       lds_copy16(src + k, lane_bytes, __builtin_amdgcn_readfirstlane(buf + (uint32_t)f * 1024));
     }
@@ -1269,6 +1272,8 @@ int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int r
       return launch_dma<128, 2, 4>(stream, args, prec, rows_bound, cus, forced_ksplit);
     case 16:  // BM 256 x BN 256, 2 x 4 waves, each 128 rows x 64 features
       return launch_dma<256, 2, 4>(stream, args, prec, rows_bound, cus, forced_ksplit);
+    case 18:  // BM 192 x BN 256, 2 x 4 waves, each 96 rows x 64 features (28 copies, 4 per wave)
+      return launch_dma<192, 2, 4>(stream, args, prec, rows_bound, cus, forced_ksplit);
     default:
       return launch_config<4, 4, 2, 2, 1, 2>(stream, args, prec, rows_bound, cus, 8, forced_ksplit);
       break;
@@ -1315,9 +1320,11 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cu
     return {config, deferred ? std::min(rounded(220.0 / tiles), cap) : 0};
   }
   if (wide && !deferred && rows >= 192 && rows <= 768) {
-    // Both operands copied to LDS: 128-row tiles with eight waves up to 447 rows, 256-row
-    // tiles from 448.
-    return {rows < 448 ? 15 : 16, 1};
+    // Both operands copied to LDS, with the tile height that fits the rows in the fewest
+    // rounds of workgroups over the CUs (gate+up of Qwen3-4B, 76 weight tiles: 128-row tiles
+    // up to 384 rows, 192-row tiles (three row tiles, 228 workgroups) up to 576, 256-row
+    // tiles above).
+    return {rows <= 384 ? 15 : rows <= 576 ? 18 : 16, 1};
   }
   const int bm = rows >= 384 || (wide && rows >= 192) ? 128 : 64;
   const int config = bm == 128 ? 9 : 12;

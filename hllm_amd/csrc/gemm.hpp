@@ -45,8 +45,8 @@ int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bou
 // An explicit configuration of the table in gemm.hip (tuning), optionally forcing the K split.
 int launch_gemm_config(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus,
                         int config, int forced_ksplit);
-// Highest configuration id of the table.
-constexpr int kGemmConfigs = 17;
+// Highest configuration id of the table (17 is not a table entry: see kDecodeConfig).
+constexpr int kGemmConfigs = 18;
 // Forced configuration meaning "the decode kernel wherever it applies" (F16, at most 64 rows,
 // deferred K splits or SwiGLU); other projections keep the choice by shape.
 constexpr int kDecodeConfig = 17;

@@ -245,7 +245,7 @@ hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captur
 hllm_status hllm_rocm_measure_read_bandwidth(int32_t device, uint64_t bytes, double* gb_s);
 
 /* Tuning and test hook, process-wide: every later projection GEMM uses configuration
- * `config` of the kernel table (0 .. 17; 17: the decode kernel for every F16 projection of at
+ * `config` of the kernel table (0 .. 18; 17: the decode kernel for every F16 projection of at
  * most 64 rows whose K splits are summed by the consumer or that applies SwiGLU) instead of the
  * choice by shape; -1 restores the
  * choice by shape. *previous (may be NULL) receives the value replaced. Results stay within

@@ -73,7 +73,7 @@ def test_calls_without_a_stage_fail_cleanly():
 def test_gemm_configuration_hook_validates_and_restores():
     previous = capi.set_gemm_config(-1)
     assert capi.set_gemm_config(previous) == -1
-    for bad in (-2, 18):
+    for bad in (-2, 19):
         with pytest.raises(capi.StageError) as e:
             capi.set_gemm_config(bad)
         assert e.value.status == capi.INVALID_REQUEST

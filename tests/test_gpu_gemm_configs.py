@@ -1,8 +1,8 @@
 """Every projection GEMM forced onto one configuration of the kernel table (through
 hllm_rocm_set_gemm_config): a ragged pass with a 512-token prefill chunk and decode rows, then
 a decode pass, of a Qwen3-0.6B-shaped two-layer slice in F16 execution, against the F32 CPU
-oracle run per sequence. Covers the configurations that copy both operands into LDS (128- and
-256-row tiles, four and eight waves), the activation-staged kernel (9), the decode kernel
+oracle run per sequence. Covers the configurations that copy both operands into LDS (128-,
+192- and 256-row tiles, four and eight waves), the activation-staged kernel (9), the decode kernel
 (17: the projections it takes in passes of at most 64 rows) and the choice by shape (-1) on
 every epilogue: deferred K-split partials (q/k/v), residual accumulation (o, down), SwiGLU
 (gate+up) and plain stores (LM head), for row counts from 2 to 554. Bounds: max-abs <= 2e-2
@@ -65,7 +65,7 @@ def stage():
     st.close()
 
 
-@pytest.mark.parametrize("config", [-1, 9, 14, 15, 16, 17])
+@pytest.mark.parametrize("config", [-1, 9, 14, 15, 16, 17, 18])
 def test_forced_configuration_matches_the_oracle(stage, expected, config):
     prompts, first, logits, tokens, second = expected
     _say("gemm configuration", config)
