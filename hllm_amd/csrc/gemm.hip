@@ -696,29 +696,31 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
       for (int n = 0; n < NF; ++n) acc[i][n] = mfma(w[n], x[i], acc[i][n]);
   };
 
-  // Copies are issued in k-step order and only for k-steps < stages: 0 .. NS - 3 before
-  // the loop, then st + NS - 2 and st + NS - 1 after the barrier at pair st (even), into
-  // the buffers of st - 2 and st - 1. At that barrier k-steps st + 1 and st + 2 must have
-  // landed; when all of st + 3 .. st + NS - 3 were issued, NS - 5 k-steps may stay in
-  // flight, otherwise none. Every LDS read a wave issued has returned before it reaches
-  // the barrier (the last group was issued a half-iteration of MFMAs earlier), so the
-  // refilled buffers are free, and the register sets are complete when their MFMAs start.
-  for (int st = 0; st < NS - 2; ++st)
+  // Copies are issued in k-step order and only for k-steps < stages: 0 .. NS - 2 before
+  // the loop, then st + NS - 1 and st + NS after the barrier at pair st (even), into the
+  // buffers of st - 1 and st, whose k-steps were read into registers during pair st - 2
+  // (st's before the loop for st = 0). At that barrier k-steps st + 1 and st + 2 must have
+  // landed; when all of st + 3 .. st + NS - 2 were issued, NS - 4 k-steps may stay in
+  // flight, otherwise none. A copy issued at barrier st is needed at barrier st + 4: two
+  // pairs of MFMAs cover its latency. Every LDS read a wave issued has returned before it
+  // reaches the barrier (the last group was issued a half-iteration of MFMAs earlier), so
+  // the refilled buffers are free, and the register sets are complete when their MFMAs start.
+  for (int st = 0; st < NS - 1; ++st)
     if (st < stages) issue(st);
-  if (stages >= NS - 2)
-    stage_barrier<(NS - 3) * kPer, 0>();
+  if (stages >= NS - 1)
+    stage_barrier<(NS - 2) * kPer, 0>();
   else
     stage_barrier<0, 0>();
   half8 xa[MF], wa[NF], xb[MF], wb[NF];
   read(0, xa, wa);
   for (int st = 0; st < stages; st += 2) {
     wait_counts<63, 0>();  // on both paths below; stated once for the compiler's benefit
-    if (st + NS - 3 < stages)
-      stage_barrier<(NS - 5) * kPer, 0>();
+    if (st + NS - 2 < stages)
+      stage_barrier<(NS - 4) * kPer, 0>();
     else
       stage_barrier<0, 0>();
-    if (st + NS - 2 < stages) issue(st + NS - 2);
     if (st + NS - 1 < stages) issue(st + NS - 1);
+    if (st + NS < stages) issue(st + NS);
     // Each register set is read a whole half-iteration of MFMAs before it is used; the
     // scheduling barriers keep the compiler from sinking the reads next to their uses, and
     // the explicit waits (on reads issued that long ago) keep it from waiting on the
