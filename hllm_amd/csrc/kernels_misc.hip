@@ -317,40 +317,68 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   const int head_first = blockIdx.y * waves + wave;  // one head per wave
   const int D = head_dim, half = D / 2;
   constexpr int per_lane = PER;
-  const int position = row_position[r];
-  const int slot = row_slot[r];
+  // The row's position and slot were written by the pack kernel: scalar loads.
+  const int position = uniform_load(row_position + r);
+  const int slot = uniform_load(row_slot + r);
   const float* row = qkv + (size_t)r * heads * D;
   const float* cos_row = rope_cos + (size_t)position * half;
   const float* sin_row = rope_sin + (size_t)position * half;
   for (int head = head_first; head < heads; head += waves * gridDim.y) {
     const bool is_q = head < q_heads;
     const bool is_v = head >= q_heads + kv_heads;
-    // Loads are unconditional (lanes past D re-read element D - 1) and every load of a step
-    // is in flight before any is used: the kernel is latency-bound.
+    // Every load of the head is issued before any is used (the partials of the first four
+    // K splits, the norm weights and the RoPE factors), unconditionally at valid addresses
+    // (lanes past D re-read element D - 1): the kernel is a short latency-bound chain.
     int dd[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) dd[j] = min(lane + 64 * j, D - 1);
+    const size_t at = (size_t)r * heads * D + (size_t)head * D;
+    float p[4][PER];
+    if (parts.parts > 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) p[u][j] = parts.data[(size_t)min(u, parts.parts - 1) * parts.stride + at + dd[j]];
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) p[0][j] = row[head * D + dd[j]];
+    }
+    const float* w = is_q ? q_norm : k_norm;
+    float wv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) wv[j] = w && !is_v ? w[dd[j]] : 1.0f;
+    // RoPE factors: for D >= 128 the lane's first-half elements lane + 64 j (j < PER / 2),
+    // for D <= 64 element lane mod D / 2.
+    float cr[PER], sr[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = D >= 128 ? min(lane + 64 * j, half - 1) : (lane & (half - 1));
+      cr[j] = cos_row[e];
+      sr[j] = sin_row[e];
+    }
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (parts.parts > 0) {
       // K-split partials of the projection, summed in split order from zero (the reduce
       // kernel's order for a plain store).
-      const size_t at = (size_t)r * heads * D + (size_t)head * D;
-      for (int s0 = 0; s0 < parts.parts; s0 += 4) {
-        float p[4][PER];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = u < parts.parts ? v[j] + p[u][j] : v[j];
+      for (int s0 = 4; s0 < parts.parts; s0 += 4) {  // splits past the first four
+        float q[4][PER];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
           for (int j = 0; j < PER; ++j)
-            p[u][j] = parts.data[(size_t)min(s0 + u, parts.parts - 1) * parts.stride + at + dd[j]];
+            q[u][j] = parts.data[(size_t)min(s0 + u, parts.parts - 1) * parts.stride + at + dd[j]];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int j = 0; j < PER; ++j) v[j] = s0 + u < parts.parts ? v[j] + p[u][j] : v[j];
+          for (int j = 0; j < PER; ++j) v[j] = s0 + u < parts.parts ? v[j] + q[u][j] : v[j];
       }
     } else {
-      const float* src = row + head * D;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) v[j] = src[dd[j]];
+      for (int j = 0; j < PER; ++j) v[j] = p[0][j];
     }
     float squares = 0.0f;
 #pragma unroll
@@ -359,20 +387,18 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
       squares += v[j] * v[j];
     }
     if (!is_v) {
-      const float* w = is_q ? q_norm : k_norm;
       if (w) {
         squares = wave_sum(squares);
         const float inverse = 1.0f / sqrtf(squares / (float)D + eps);
 #pragma unroll
-        for (int j = 0; j < PER; ++j) v[j] = v[j] * (inverse * w[dd[j]]);  // lanes past D hold 0
+        for (int j = 0; j < PER; ++j) v[j] = v[j] * (inverse * wv[j]);  // lanes past D hold 0
       }
       if (D >= 128) {
         const int pairs = per_lane / 2;  // elements [0, pairs) are first halves
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           if (j < pairs) {
-            const int d = lane + 64 * j;
-            const float c = cos_row[d], s = sin_row[d];
+            const float c = cr[j], s = sr[j];
             const float a = v[j], b = v[j + pairs];
             v[j] = a * c - b * s;
             v[j + pairs] = b * c + a * s;
@@ -381,13 +407,11 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
       } else {
         const float partner = __shfl_xor(v[0], half, 64);
         if (lane < D) {
-          if (lane < half) {
-            const float c = cos_row[lane], s = sin_row[lane];
+          const float c = cr[0], s = sr[0];
+          if (lane < half)
             v[0] = v[0] * c - partner * s;
-          } else {
-            const float c = cos_row[lane - half], s = sin_row[lane - half];
+          else
             v[0] = v[0] * c + partner * s;
-          }
         }
       }
     }
