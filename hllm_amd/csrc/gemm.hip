@@ -1306,10 +1306,12 @@ struct Choice {
 Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cus) {
   const bool wide = n >= 16384;
   const auto rounded = [](double x) { return std::max(1, (int)(x + 0.5)); };
-  if (f16 && deferred && rows <= 768 && (rows >= 448 || (n >= 4096 && rows >= 384))) {
-    // Deferred projections of chunk-sized passes (q/k/v from 384 rows, o and down from
-    // 448): both operands copied to LDS in 128 x 256 tiles (one workgroup per CU), with the
-    // most K splits (2 to 8) whose workgroups fit every XCD's CUs at once (xcd_tile).
+  if (f16 && deferred && rows >= 224 && rows <= 768) {
+    // Deferred projections of passes from 224 rows: both operands copied to LDS in 128 x 256
+    // tiles (one workgroup per CU), with the most K splits (2 to 8) whose workgroups fit
+    // every XCD's CUs at once (xcd_tile). Measured on the Qwen3-4B projections against the
+    // activation-staged kernel: down 28 against 34-42 us from 288 to 384 rows, q/k/v 20 / 23
+    // against 24 / 27 us at 224 / 352 rows, o within 1 us.
     const int n_tiles = (n + 255) / 256, m_tiles = (rows + 127) / 128, per_xcd = std::max(1, cus / kXcds);
     int ks = 8;
     while (ks > 2 && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
