@@ -661,7 +661,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
   const char* W = reinterpret_cast<const char*>(a.w_hi) + (size_t)tile_n * (BN / 16) * frag_stride * 16;
   const uint32_t lane_bytes = (uint32_t)lane * 16;
   // K-steps come in pairs: an odd count gets one more, a copy of the last k-step whose
-  // activations are zeroed in registers before its MFMAs.
+  // MFMAs are skipped.
   const int stages = (steps + 1) & ~1;
   const int kt_last = max(kt0, kt1 - 1);
   // This wave's copies of k-step st into buffer st % NS (the caller keeps st < stages).
@@ -732,11 +732,10 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN))
     wait_counts<63, 0>();
     read(st + 2, xa, wa);  // past the last k-step this reads a buffer that is never used
     __builtin_amdgcn_sched_barrier(0);
-    if (st + 1 >= steps) {
-#pragma unroll
-      for (int i = 0; i < MF; ++i) xb[i] = half8{};
-    }
-    multiply(xb, wb);
+    // An odd step count ends on a copy of the last k-step, whose MFMAs are skipped (a
+    // workgroup-uniform branch: zeroing the operand instead costs a select per register
+    // in every pair).
+    if (st + 1 < steps) multiply(xb, wb);
   }
   // Drain the copies still in flight before the workgroup's LDS can be reused.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
