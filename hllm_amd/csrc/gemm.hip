@@ -1199,7 +1199,9 @@ int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
   if (ksplit > 1 && (!a.defer_reduce || PAIR)) fail(HLLM_INTERNAL, "decode GEMM splits K only for deferred consumers");
   if (ksplit > 1 && (size_t)ksplit * a.M * a.N > a.workspace_floats) ksplit = 1;
   a.ksplit = ksplit;
-  // A deferred projection stages its split's activations whole when they fit in LDS.
+  // A deferred projection stages its split's activations whole when they fit in LDS
+  // (HLLM_ROCM_DECODE_WHOLE=0, read at every launch: chunk by chunk, the path of K ranges
+  // that do not fit; for tests).
   const int KT = (int)(a.Kp >> 5);
   const int per = ((KT + ksplit - 1) / ksplit + KC - 1) / KC * KC;
   const size_t whole_lds = (size_t)MF * per * 1024;

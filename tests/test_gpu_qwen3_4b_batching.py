@@ -6,10 +6,14 @@ with the full vocabulary, against the F32 CPU oracle:
   [16, 2048]) with the projection GEMMs chosen by shape, and with each of the decode
   configurations forced (0, 1, 2: register-streaming tiles of 16/32/64 rows; 12:
   activation-staged 64 x 256 tiles; 17: the decode kernel, one weight stream per wave with
-  gate/up pairs and a SwiGLU register epilogue);
+  gate/up pairs and a SwiGLU register epilogue), and the decode kernel once more with its
+  deferred projections staging their activations chunk by chunk instead of whole
+  (HLLM_ROCM_DECODE_WHOLE=0: the path for K ranges that do not fit in LDS);
 * one pass mixing a 512-token prefill chunk of a new sequence with the same 64 decode rows.
 
 Per row: last-layer hidden state and logits within max-abs 2e-2 and cosine 0.9999."""
+import os
+
 import numpy as np
 import pytest
 
@@ -89,6 +93,29 @@ def test_64_decode_rows_match_the_oracle(world, config):
     hp.check_rows(out["trace"][-1], w["hidden"], f"config {config} hidden")
     hp.check_rows(out["logits"], w["logits"], f"config {config} logits")
     hp.greedy_agrees(out["tokens"], w["logits"], out["logits"], f"config {config}")
+    for s in seqs:
+        st.release(s)
+
+
+def test_64_decode_rows_with_chunked_activation_staging_match_the_oracle(world):
+    w, st = world, world["stage"]
+    hp.say("qwen3-4b 64 decode rows, decode kernel with chunked activation staging")
+    seqs = _fresh_sequences(w)
+    previous = capi.set_gemm_config(17)
+    before = os.environ.get("HLLM_ROCM_DECODE_WHOLE")
+    os.environ["HLLM_ROCM_DECODE_WHOLE"] = "0"  # read by the launcher at every launch
+    try:
+        out = st.execute(_decode_items(seqs, w["lengths"]), token_ids=w["decode_ids"], want_logits=True,
+                         trace=True)
+    finally:
+        capi.set_gemm_config(previous)
+        if before is None:
+            del os.environ["HLLM_ROCM_DECODE_WHOLE"]
+        else:
+            os.environ["HLLM_ROCM_DECODE_WHOLE"] = before
+    hp.check_rows(out["trace"][-1], w["hidden"], "chunked staging hidden")
+    hp.check_rows(out["logits"], w["logits"], "chunked staging logits")
+    hp.greedy_agrees(out["tokens"], w["logits"], out["logits"], "chunked staging")
     for s in seqs:
         st.release(s)
 
