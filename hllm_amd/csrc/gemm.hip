@@ -1312,11 +1312,19 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cu
     // tiles (one workgroup per CU), with the most K splits (2 to 8) whose workgroups fit
     // every XCD's CUs at once (xcd_tile). Measured on the Qwen3-4B projections against the
     // activation-staged kernel: down 28 against 34-42 us from 288 to 384 rows, q/k/v 20 / 23
-    // against 24 / 27 us at 224 / 352 rows, o within 1 us.
-    const int n_tiles = (n + 255) / 256, m_tiles = (rows + 127) / 128, per_xcd = std::max(1, cus / kXcds);
-    int ks = 8;
-    while (ks > 2 && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
-    return {15, ks};
+    // against 24 / 27 us at 224 / 352 rows, o within 1 us. 192 x 256 tiles instead when they
+    // allow at least twice the K splits (a quarter less work per workgroup): o and down of
+    // 513-576-row passes (three row tiles against five), 24.0 -> 23.4 and 43.7 -> 37.2 us;
+    // where 192-row tiles gain less they measured slower (q/k/v at 320-384 rows).
+    const int n_tiles = (n + 255) / 256, per_xcd = std::max(1, cus / kXcds);
+    const auto splits = [&](int bm) {
+      const int m_tiles = (rows + bm - 1) / bm;
+      int ks = 8;
+      while (ks > 2 && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
+      return ks;
+    };
+    const int ks128 = splits(128), ks192 = splits(192);
+    return ks192 >= 2 * ks128 ? Choice{18, ks192} : Choice{15, ks128};
   }
   if (rows <= 64 && (!wide || rows <= 32)) {
     const int config = rows <= 16 ? 0 : rows <= 32 ? 1 : 2;

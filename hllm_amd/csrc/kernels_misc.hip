@@ -174,9 +174,10 @@ __device__ inline void load8_at(const float* x, float* v) {
 // 512) threads, at most 1024; Q = 2 above 8192 columns) and keeps them in registers
 // between the square sum and the scaled store. A row is a short chain of dependent steps,
 // so the kernel is latency-bound:
-// every load of a step (the chunks, or four K-split partials of every chunk) is issued
-// unconditionally, at clamped addresses, before any is used.
-template <int Q>
+// every load of a step (the chunks, or U K-split partials of every chunk) is issued
+// unconditionally, at clamped addresses, before any is used; the launcher picks U for the
+// partial count, so few clamped loads repeat the last partial.
+template <int Q, int U>
 __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
     float* h, int hidden, const int32_t* row_index, int rows, const int32_t* device_rows,
     const float* weight, float eps, uint16_t* out_hi, uint16_t* out_lo, uint64_t cols_padded,
@@ -211,8 +212,7 @@ __global__ void __launch_bounds__(1024) rmsnorm_flayout_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[q][j] = 0.0f;
       const float* base = residual.data + (size_t)src * hidden;
-      // Up to sixteen splits' loads in flight at once (four when a thread holds two chunks).
-      constexpr int U = Q == 1 ? 16 : 4;
+      // U splits' loads in flight at once.
       for (int s0 = 0; s0 < residual.parts; s0 += U) {
         float p[U][Q][8];
 #pragma unroll
@@ -672,18 +672,26 @@ void launch_rmsnorm_flayout(hipStream_t stream, float* h, int hidden, const int3
   // Chunks of 8 columns up to the padded width (the operand's zero padding is written too).
   const int chunks = (int)((std::max<uint64_t>(hidden, cols_padded) + 7) / 8);
   const int threads = std::min(1024, (chunks + 63) / 64 * 64);
-  if (chunks <= 1024) {
-    observed("rmsnorm_flayout_kernel<1>", [&] {
-      rmsnorm_flayout_kernel<1><<<rows, threads, 0, stream>>>(h, hidden, row_index, rows, device_rows, weight, eps,
-                                                             out_hi, out_lo, cols_padded, residual);
+  const auto go = [&](auto kernel, const char* name) {
+    observed(name, [&] {
+      kernel<<<rows, threads, 0, stream>>>(h, hidden, row_index, rows, device_rows, weight, eps, out_hi, out_lo,
+                                           cols_padded, residual);
     });
-  } else {
-    if (chunks > 2 * 1024) fail(HLLM_INTERNAL, "hidden size exceeds the RMSNorm kernel");
-    observed("rmsnorm_flayout_kernel<2>", [&] {
-      rmsnorm_flayout_kernel<2><<<rows, threads, 0, stream>>>(h, hidden, row_index, rows, device_rows, weight, eps,
-                                                             out_hi, out_lo, cols_padded, residual);
-    });
-  }
+  };
+  if (chunks > 2 * 1024) fail(HLLM_INTERNAL, "hidden size exceeds the RMSNorm kernel");
+  // Partial loads in flight per thread: the partial count rounded up to 4, 8, 12 or 16 (at
+  // most sixteen, four when a thread holds two chunks; more partials take several rounds).
+  const int parts = residual.parts;
+  if (chunks > 1024)
+    go(&rmsnorm_flayout_kernel<2, 4>, "rmsnorm_flayout_kernel<2, 4>");
+  else if (parts <= 4)
+    go(&rmsnorm_flayout_kernel<1, 4>, "rmsnorm_flayout_kernel<1, 4>");
+  else if (parts <= 8)
+    go(&rmsnorm_flayout_kernel<1, 8>, "rmsnorm_flayout_kernel<1, 8>");
+  else if (parts <= 12)
+    go(&rmsnorm_flayout_kernel<1, 12>, "rmsnorm_flayout_kernel<1, 12>");
+  else
+    go(&rmsnorm_flayout_kernel<1, 16>, "rmsnorm_flayout_kernel<1, 16>");
 }
 
 void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int q_heads, int kv_heads,
