@@ -305,7 +305,8 @@ __device__ inline uint64_t kv_index(const KvView& kv, int layer, int slot, int w
 // One wave per head. Lane l holds elements d = l + 64 j. Head dimensions are powers of two
 // in [4, 256]: for D >= 128 both members of a rotate-half pair (d, d + D/2) sit in the same
 // lane; for D <= 64 the partner is lane l ^ (D/2).
-template <int PER>  // elements per lane: ceil(D / 64)
+// PER: elements per lane, ceil(D / 64); U: K-split partials loaded per round.
+template <int PER, int U>
 __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
     const float* qkv, int q_heads, int kv_heads, int head_dim, const float* q_norm,
     const float* k_norm, float eps, const float* rope_cos, const float* rope_sin,
@@ -326,17 +327,17 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
   for (int head = head_first; head < heads; head += waves * gridDim.y) {
     const bool is_q = head < q_heads;
     const bool is_v = head >= q_heads + kv_heads;
-    // Every load of the head is issued before any is used (the partials of the first four
-    // K splits, the norm weights and the RoPE factors), unconditionally at valid addresses
+    // Every load of the head is issued before any is used (the partials of the first U K
+    // splits, the norm weights and the RoPE factors), unconditionally at valid addresses
     // (lanes past D re-read element D - 1): the kernel is a short latency-bound chain.
     int dd[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) dd[j] = min(lane + 64 * j, D - 1);
     const size_t at = (size_t)r * heads * D + (size_t)head * D;
-    float p[4][PER];
+    float p[U][PER];
     if (parts.parts > 0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int j = 0; j < PER; ++j) p[u][j] = parts.data[(size_t)min(u, parts.parts - 1) * parts.stride + at + dd[j]];
     } else {
@@ -361,18 +362,18 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
       // K-split partials of the projection, summed in split order from zero (the reduce
       // kernel's order for a plain store).
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int j = 0; j < PER; ++j) v[j] = u < parts.parts ? v[j] + p[u][j] : v[j];
-      for (int s0 = 4; s0 < parts.parts; s0 += 4) {  // splits past the first four
-        float q[4][PER];
+      for (int s0 = U; s0 < parts.parts; s0 += U) {  // splits past the first U
+        float q[U][PER];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int j = 0; j < PER; ++j)
             q[u][j] = parts.data[(size_t)min(s0 + u, parts.parts - 1) * parts.stride + at + dd[j]];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int j = 0; j < PER; ++j) v[j] = s0 + u < parts.parts ? v[j] + q[u][j] : v[j];
       }
@@ -707,12 +708,14 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
                                           row_position, row_slot, kv, layer, q_out, qkv_parts);
     });
   };
+  // Two partials per round when the projection has at most two (no clamped repeats).
+  const bool two = qkv_parts.parts <= 2;
   if (head_dim <= 64)
-    go(&qkv_rope_append_kernel<1>);
+    two ? go(&qkv_rope_append_kernel<1, 2>) : go(&qkv_rope_append_kernel<1, 4>);
   else if (head_dim <= 128)
-    go(&qkv_rope_append_kernel<2>);
+    two ? go(&qkv_rope_append_kernel<2, 2>) : go(&qkv_rope_append_kernel<2, 4>);
   else if (head_dim <= 256)
-    go(&qkv_rope_append_kernel<4>);
+    two ? go(&qkv_rope_append_kernel<4, 2>) : go(&qkv_rope_append_kernel<4, 4>);
   else
     fail(HLLM_INTERNAL, "head dimension exceeds the RoPE kernel");
 }
