@@ -1376,9 +1376,10 @@ int env_int(const char* name, int fallback) {
 // rows (weights streamed from HBM, launches back to back): waves per workgroup, the waves per
 // CU the K split aims at, the weight ring depth, the staged chunk (k-steps) and the fragment
 // rows per wave. Deferred projections: eight waves of one fragment row, chunks of four;
-// gate/up pairs: four waves, chunks of eight. HLLM_ROCM_DECODE_WAVES / _TARGET / _RING /
-// _CHUNK / _FRAGS override the deferred shape, HLLM_ROCM_DECODE_PAIR_WAVES / _PAIR_CHUNK the
-// paired one, for sweeps.
+// gate/up pairs: four waves, chunks of sixteen through a ring of eight (chunks of eight:
+// 25.9 against 24.9 us for Qwen3-4B at 64 rows; a ring of sixteen 26.0).
+// HLLM_ROCM_DECODE_WAVES / _TARGET / _RING / _CHUNK / _FRAGS override the deferred shape,
+// HLLM_ROCM_DECODE_PAIR_WAVES / _PAIR_CHUNK the paired one, for sweeps.
 struct DecodeShape {
   int waves, target_waves_per_cu, ring, chunk, frags;
 };
@@ -1387,7 +1388,7 @@ const DecodeShape& decode_shape(bool pair) {
                                     env_int("HLLM_ROCM_DECODE_RING", 4), env_int("HLLM_ROCM_DECODE_CHUNK", 4),
                                     env_int("HLLM_ROCM_DECODE_FRAGS", 1)};
   static const DecodeShape paired{env_int("HLLM_ROCM_DECODE_PAIR_WAVES", 4), 0, 8,
-                                  env_int("HLLM_ROCM_DECODE_PAIR_CHUNK", 8), 2};
+                                  env_int("HLLM_ROCM_DECODE_PAIR_CHUNK", 16), 2};
   return pair ? paired : deferred;
 }
 
@@ -1431,7 +1432,8 @@ template <int MF>
 int launch_decode_rows(hipStream_t stream, const GemmArgs& a, int cus) {
   const DecodeShape& d = decode_shape(a.epilogue == kEpiSwiglu);
   if (d.chunk <= 4) return launch_decode_variant<MF, 4, 4>(stream, a, cus);
-  return launch_decode_variant<MF, 8, 8>(stream, a, cus);
+  if (d.chunk <= 8) return launch_decode_variant<MF, 8, 8>(stream, a, cus);
+  return launch_decode_variant<MF, 16, 8>(stream, a, cus);
 }
 
 int launch_decode(hipStream_t stream, const GemmArgs& a, int rows, int cus) {
