@@ -179,16 +179,24 @@ class Engine:
 
     def prestart(self, rng, vocab, max_rows):
         """Brings the engine to its steady state before any timed step: `concurrency`
-        requests of the stream are admitted at once, each already `g ~ U[0, out_len)`
-        tokens into its output (the ages of requests that have been running for a while),
-        with its prompt and those tokens prefilled by untimed passes of up to `max_rows`
-        rows (random IDs stand in for the generated tokens: only the cache contents and
-        lengths matter to later steps). Each request's last prefill row samples, so its next
+        requests of the stream are admitted at once, each with an output length drawn in
+        proportion to its length from the stream's U[64, 256] and already `g ~ U[0,
+        out_len)` tokens into it. A request running at a random moment is length-biased
+        (long ones run more of the time) and uniformly aged, so the pre-started batch
+        completes requests at the steady rate from its first step (with unbiased lengths
+        it completes them almost twice as fast at first: a burst of prefill passes, then a
+        lull, for a few hundred steps). Each request comes with its prompt and those tokens
+        prefilled by untimed passes of up to `max_rows` rows (random IDs stand in for the
+        generated tokens: only the cache contents and lengths matter to later steps). Each request's last prefill row samples, so its next
         input comes from the device like every decode row's."""
         pieces = []  # (sequence, first position, token IDs, samples)
         while len(self.active) < self.concurrency:
             r = self.next_req
             self.next_req = next(self.stream)
+            while True:  # length-biased output length: accept L with probability L / 256
+                r.out_len = int(rng.integers(64, 257))
+                if rng.random() * 256 < r.out_len:
+                    break
             g = int(rng.integers(0, r.out_len))
             r.seq = self.stage.allocate(len(r.prompt) + r.out_len)
             history = np.concatenate([r.prompt, rng.integers(0, vocab, g, dtype=np.uint64)])
