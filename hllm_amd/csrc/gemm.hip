@@ -1316,24 +1316,36 @@ struct Choice {
 Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cus) {
   const bool wide = n >= 16384;
   const auto rounded = [](double x) { return std::max(1, (int)(x + 0.5)); };
-  if (f16 && deferred && rows >= 224 && rows <= 768) {
-    // Deferred projections of passes from 224 rows: both operands copied to LDS in 128 x 256
-    // tiles (one workgroup per CU), with the most K splits (2 to 8) whose workgroups fit
-    // every XCD's CUs at once (xcd_tile). Measured on the Qwen3-4B projections against the
-    // activation-staged kernel: down 28 against 34-42 us from 288 to 384 rows, q/k/v 20 / 23
-    // against 24 / 27 us at 224 / 352 rows, o within 1 us. 192 x 256 tiles instead when they
-    // allow at least twice the K splits (a quarter less work per workgroup): o and down of
-    // 513-576-row passes (three row tiles against five), 24.0 -> 23.4 and 43.7 -> 37.2 us;
-    // where 192-row tiles gain less they measured slower (q/k/v at 320-384 rows).
+  if (f16 && deferred && rows > 64 && rows <= 768) {
+    // Deferred projections of chunk-sized F16 passes, with the most K splits whose
+    // workgroups fit every XCD's CUs at once (xcd_tile; one workgroup per CU: a second round
+    // costs up to a third more, q/k/v at 160 rows 18.4 -> 24.1 us).
     const int n_tiles = (n + 255) / 256, per_xcd = std::max(1, cus / kXcds);
-    const auto splits = [&](int bm) {
+    const auto splits = [&](int bm, int least, int most) {
       const int m_tiles = (rows + bm - 1) / bm;
-      int ks = 8;
-      while (ks > 2 && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
+      int ks = most;
+      while (ks > least && (n_tiles * ks + kXcds - 1) / kXcds * m_tiles > per_xcd) --ks;
       return ks;
     };
-    const int ks128 = splits(128), ks192 = splits(192);
-    return ks192 >= 2 * ks128 ? Choice{18, ks192} : Choice{15, ks128};
+    if (rows >= 224) {
+      // From 224 rows both operands are copied to LDS in 128 x 256 tiles (2 to 8 splits).
+      // Measured on the Qwen3-4B projections against the activation-staged kernel: down 28
+      // against 34-42 us from 288 to 384 rows, q/k/v 20 / 23 against 24 / 27 us at 224 /
+      // 352 rows, o within 1 us. 192 x 256 tiles instead when they allow at least twice the
+      // K splits (a quarter less work per workgroup): o and down of 513-576-row passes
+      // (three row tiles against five), 24.0 -> 23.4 and 43.7 -> 37.2 us; where 192-row
+      // tiles gain less they measured slower (q/k/v at 320-384 rows).
+      const int ks128 = splits(128, 2, 8), ks192 = splits(192, 2, 8);
+      return ks192 >= 2 * ks128 ? Choice{18, ks192} : Choice{15, ks128};
+    }
+    // 65-223 rows: 64-row activation-staged tiles (at least two chunks per split), or the
+    // 128-row LDS-copy tiles where they allow more than twice the K splits (less work per
+    // workgroup). Measured at 96-208 rows: o 12.0-15.3 us, down 21.5-26.7, q/k/v 13.8-18.3
+    // (q/k/v at 160-208 rows 24-28 us with the earlier rule of ~280 workgroups, which took
+    // a second round of workgroups on some XCDs).
+    const int ks64 = splits(64, 1, std::min(8, std::max(1, (int)(kp >> 5) / 16)));
+    const int ks128 = splits(128, 2, 8);
+    return 2 * ks64 < ks128 ? Choice{15, ks128} : Choice{12, ks64};
   }
   if (rows <= 64 && (!wide || rows <= 32)) {
     const int config = rows <= 16 ? 0 : rows <= 32 ? 1 : 2;
@@ -1341,14 +1353,15 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cu
     const int cap = std::max(1, (int)(kp >> 5) / 8);  // at least two k-steps per K-wave
     return {config, deferred ? std::min(rounded(220.0 / tiles), cap) : 0};
   }
-  if (wide && !deferred && rows >= 192 && rows <= 768) {
+  if (wide && !deferred && rows > 192 && rows <= 768) {
     // Both operands copied to LDS, with the tile height that fits the rows in the fewest
     // rounds of workgroups over the CUs (gate+up of Qwen3-4B, 76 weight tiles: 128-row tiles
     // up to 384 rows, 192-row tiles (three row tiles, 228 workgroups) up to 576, 256-row
-    // tiles above).
+    // tiles above). Up to 192 rows the activation-staged 64-row tiles fit in one round
+    // (228 workgroups): 35.8 against 45.3 us at 192 rows.
     return {rows <= 384 ? 15 : rows <= 576 ? 18 : 16, 1};
   }
-  const int bm = rows >= 384 || (wide && rows >= 192) ? 128 : 64;
+  const int bm = rows >= 384 || (wide && rows > 192) ? 128 : 64;
   const int config = bm == 128 ? 9 : 12;
   const int kc = bm == 128 ? 4 : 8;
   const long tiles = (long)((n + 255) / 256) * ((rows + bm - 1) / bm);
