@@ -1332,11 +1332,13 @@ Choice gemm_choice(int rows, int n, uint64_t kp, bool deferred, bool f16, int cu
       // Measured on the Qwen3-4B projections against the activation-staged kernel: down 28
       // against 34-42 us from 288 to 384 rows, q/k/v 20 / 23 against 24 / 27 us at 224 /
       // 352 rows, o within 1 us. 192 x 256 tiles instead when they allow at least twice the
-      // K splits (a quarter less work per workgroup): o and down of 513-576-row passes
-      // (three row tiles against five), 24.0 -> 23.4 and 43.7 -> 37.2 us; where 192-row
-      // tiles gain less they measured slower (q/k/v at 320-384 rows).
+      // K splits (a quarter less work per workgroup) and those splits still hold 32 k-steps
+      // or more: down of 513-576-row passes (three row tiles against five), 43.7 -> 37.2 us.
+      // Where 192-row tiles gain less they measured slower (q/k/v at 320-384 rows), and o
+      // (16 k-steps per split) gains 0.6 us while its consumer reads twice the partials.
       const int ks128 = splits(128, 2, 8), ks192 = splits(192, 2, 8);
-      return ks192 >= 2 * ks128 ? Choice{18, ks192} : Choice{15, ks128};
+      const bool long_splits = (int)(kp >> 5) / ks192 >= 32;
+      return ks192 >= 2 * ks128 && long_splits ? Choice{18, ks192} : Choice{15, ks128};
     }
     // 65-223 rows: 64-row activation-staged tiles (at least two chunks per split), or the
     // 128-row LDS-copy tiles where they allow more than twice the K splits (less work per
