@@ -717,9 +717,10 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
   const int heads = q_heads + 2 * kv_heads;
   // Two partials per round when the projection has at most two (no clamped repeats), then
   // with three heads per wave (four waves per block: 16 waves per Qwen3 row of 48 heads;
-  // 15.8 -> 14.1 us at 575 rows); four partials per round and one head per wave otherwise
-  // (three heads per wave measured 10% slower there).
-  const bool two = qkv_parts.parts <= 2;
+  // 15.8 -> 14.1 us at 575 rows); four or eight partials per round (one round for up to
+  // eight) and one head per wave otherwise (three heads per wave measured 10% slower there).
+  const int parts = qkv_parts.parts;
+  const bool two = parts <= 2;
   const int hb = two ? 3 : 1;
   const dim3 grid(rows, (heads + 4 * hb - 1) / (4 * hb));
   const auto go = [&](auto kernel) {
@@ -729,11 +730,14 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
     });
   };
   if (head_dim <= 64)
-    two ? go(&qkv_rope_append_kernel<1, 2, 3>) : go(&qkv_rope_append_kernel<1, 4, 1>);
+    two ? go(&qkv_rope_append_kernel<1, 2, 3>) : parts <= 4 ? go(&qkv_rope_append_kernel<1, 4, 1>)
+                                                              : go(&qkv_rope_append_kernel<1, 8, 1>);
   else if (head_dim <= 128)
-    two ? go(&qkv_rope_append_kernel<2, 2, 3>) : go(&qkv_rope_append_kernel<2, 4, 1>);
+    two ? go(&qkv_rope_append_kernel<2, 2, 3>) : parts <= 4 ? go(&qkv_rope_append_kernel<2, 4, 1>)
+                                                              : go(&qkv_rope_append_kernel<2, 8, 1>);
   else if (head_dim <= 256)
-    two ? go(&qkv_rope_append_kernel<4, 2, 3>) : go(&qkv_rope_append_kernel<4, 4, 1>);
+    two ? go(&qkv_rope_append_kernel<4, 2, 3>) : parts <= 4 ? go(&qkv_rope_append_kernel<4, 4, 1>)
+                                                              : go(&qkv_rope_append_kernel<4, 8, 1>);
   else
     fail(HLLM_INTERNAL, "head dimension exceeds the RoPE kernel");
 }
