@@ -87,6 +87,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     }
   }
   const int32_t* table = block_table + (size_t)it.sequence * table_width;
+  const int group = out.attn_group, qb = out.attn_work ? attn_block_rows(group) : 1;
   for (int j = threadIdx.x; j < (int)it.query_tokens; j += blockDim.x) {
     const int r = offset + j;
     const int position = (int)it.first_position + j;
@@ -95,24 +96,50 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     out.row_slot[r] = table[position / block_tokens] * block_tokens + position % block_tokens;
     out.row_token[r] = (it.flags & HLLM_ITEM_TOKEN_FROM_DEVICE) ? last_token[it.sequence]
                                                                  : host_tokens[r];
+    if (out.attn_work) {
+      // The key splits of the row's attention block (as the work items below count them).
+      const int r0 = j / qb * qb, rows = min(qb, (int)it.query_tokens - r0);
+      const int keys = (int)it.first_position + r0 + rows;
+      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
+      out.row_splits[r] = (keys + per - 1) / per;
+    }
   }
   // Attention blocks of this item: query rows [r0, r0 + rows) against keys [0, first + r0 + rows),
-  // the last block (most keys) first.
-  if (out.attn_work && threadIdx.x == 0) {
-    const int group = out.attn_group, qb = attn_block_rows(group);
+  // the last block (most keys) first (the rows' split counts are written above, one thread
+  // per row). Wave 0 takes 64 blocks at a time, a lane per block in list order; a block's
+  // first slot in its class is the class's next slot plus the splits of the lanes before
+  // it in that class (a scan over the wave).
+  if (out.attn_work && threadIdx.x < 64) {
+    const int lane = threadIdx.x;
     const int q = (int)it.query_tokens, first = (int)it.first_position;
-    for (int r0 = (q - 1) / qb * qb; r0 >= 0; r0 -= qb) {
+    const int nblocks = (q + qb - 1) / qb;
+    for (int k0 = 0; k0 < nblocks; k0 += 64) {
+      const int k = k0 + lane;
+      const bool valid = k < nblocks;
+      const int r0 = valid ? (nblocks - 1 - k) * qb : 0;
       const int rows = min(qb, q - r0);
       const int keys = first + r0 + rows;
       const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
-      const int splits = (keys + per - 1) / per;
+      const int splits = valid ? (keys + per - 1) / per : 0;
       const int cls = attn_work_class(per, rows * group, out.attn_decode_unit);
-      for (int s = 0; s < splits; ++s)
-        out.attn_work[next[cls]++] = AttnWork{i, offset + r0, rows, first + r0, s, splits, s * per,
-                                              min(keys, (s + 1) * per)};
-      for (int r = 0; r < rows; ++r) out.row_splits[offset + r0 + r] = splits;
+#pragma unroll
+      for (int c = 0; c < kAttnClasses; ++c) {
+        const int mine = cls == c ? splits : 0;
+        int incl = mine;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int t = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += t;
+        }
+        if (mine > 0) {
+          const int slot = next[c] + incl - mine;
+          for (int sp = 0; sp < splits; ++sp)
+            out.attn_work[slot + sp] = AttnWork{i, offset + r0, rows, first + r0, sp, splits, sp * per,
+                                                min(keys, (sp + 1) * per)};
+        }
+        next[c] += __shfl(incl, 63, 64);
+      }
     }
-    if (i == n_items - 1) *out.attn_count = total;
+    if (i == n_items - 1 && lane == 0) *out.attn_count = total;
   }
 }
 
