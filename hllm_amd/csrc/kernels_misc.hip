@@ -157,9 +157,16 @@ __global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* hi, const
     const half8 vh = *reinterpret_cast<const half8*>(hi + at);
     half8 vl = {};
     if (lo) vl = *reinterpret_cast<const half8*>(lo + at);
+    float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (c + j < hidden) out[c + j] = (float)vh[j] + (float)vl[j] * kLoUnscale;
+    for (int j = 0; j < 8; ++j) v[j] = (float)vh[j] + (float)vl[j] * kLoUnscale;
+    if (c + 8 <= hidden && (hidden & 3) == 0) {  // two 16-byte stores
+      *reinterpret_cast<floatx4*>(out + c) = floatx4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<floatx4*>(out + c + 4) = floatx4{v[4], v[5], v[6], v[7]};
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c + j < hidden) out[c + j] = v[j];
     }
   }
 }
@@ -509,15 +516,29 @@ __global__ void __launch_bounds__(kBlock) argmax_partial_kernel(const float* log
   __shared__ int si[4];
   const int r = blockIdx.x, part = blockIdx.y;
   if (r >= *device_rows) return;
-  const int chunk = (cols + parts - 1) / parts;
+  // Parts of whole 4-column groups when the row allows 16-byte loads (the first maximum
+  // does not depend on how the columns are dealt).
+  const bool vec = (cols & 3) == 0 && ((uintptr_t)logits & 15) == 0;
+  const int chunk = vec ? ((cols + parts - 1) / parts + 3) & ~3 : (cols + parts - 1) / parts;
   const int c0 = part * chunk, c1 = min(cols, c0 + chunk);
   const float* row = logits + (size_t)r * cols;
   Best best{-INFINITY, 0x7fffffff};
   bool bad = false;
-  for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
-    const float x = row[c];
-    bad |= !isfinite(x);
-    best = better(best, Best{x, c});
+  if (vec) {
+    for (int c = c0 + 4 * (int)threadIdx.x; c < c1; c += 4 * (int)blockDim.x) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(row + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bad |= !isfinite(x[j]);
+        best = better(best, Best{x[j], c + j});
+      }
+    }
+  } else {
+    for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
+      const float x = row[c];
+      bad |= !isfinite(x);
+      best = better(best, Best{x, c});
+    }
   }
   if (bad) atomicOr(flags, 2);
   best = wave_best(best);
