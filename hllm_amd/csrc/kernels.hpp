@@ -220,9 +220,12 @@ bool attention_uses_mfma(int head_dim, bool kv_f32);
 
 // Row-wise first maximum over `cols` F32 values per row (greedy sampling) and a
 // non-finite flag (bit 1 of flags).
+// With `last_token` set, each row's token is also recorded as its sequence's last token
+// (as launch_record_tokens does: sample_item maps sampled rows to items).
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
                    int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
-                   int32_t* flags);
+                   int32_t* flags, const int32_t* sample_item = nullptr, const ItemMeta* items = nullptr,
+                   int32_t* last_token = nullptr);
 
 // Temperature / top-k / top-p sampling and log-probabilities of sampled rows whose item
 // asks for either (runtime::sample_token, cpp/src/sampling.cpp:19-89); greedy rows without

@@ -557,7 +557,8 @@ __global__ void __launch_bounds__(kBlock) argmax_partial_kernel(const float* log
 }
 
 __global__ void argmax_final_kernel(const int32_t* device_rows, int parts, const float* part_val,
-                                    const int32_t* part_idx, int32_t* tokens) {
+                                    const int32_t* part_idx, int32_t* tokens, const int32_t* sample_item,
+                                    const ItemMeta* items, int32_t* last_token) {
   const int r = blockIdx.x;
   if (r >= *device_rows) return;
   Best best{-INFINITY, 0x7fffffff};
@@ -565,7 +566,11 @@ __global__ void argmax_final_kernel(const int32_t* device_rows, int parts, const
     best = better(best, Best{part_val[(size_t)r * parts + p], part_idx[(size_t)r * parts + p]});
   }
   best = wave_best(best);
-  if (threadIdx.x == 0) tokens[r] = best.index == 0x7fffffff ? 0 : best.index;
+  if (threadIdx.x == 0) {
+    const int token = best.index == 0x7fffffff ? 0 : best.index;
+    tokens[r] = token;
+    if (last_token) last_token[items[sample_item[r]].sequence] = token;
+  }
 }
 
 __global__ void record_tokens_kernel(const int32_t* tokens, const int32_t* sample_item,
@@ -792,12 +797,15 @@ void launch_qkv_rope_append(hipStream_t stream, const float* qkv, int rows, int 
 
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,
                    int cols, float* part_val, int32_t* part_idx, int parts, int32_t* tokens,
-                   int32_t* flags) {
+                   int32_t* flags, const int32_t* sample_item, const ItemMeta* items, int32_t* last_token) {
   if (max_rows <= 0) return;
   observed("argmax_partial_kernel", [&] { argmax_partial_kernel<<<dim3(max_rows, parts), kBlock, 0, stream>>>(logits, device_rows, cols,
                                                                       parts, part_val, part_idx,
                                                                       flags); });
-  observed("argmax_final_kernel", [&] { argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens); });
+  observed("argmax_final_kernel", [&] {
+    argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens, sample_item, items,
+                                                     last_token);
+  });
 }
 
 void launch_record_tokens(hipStream_t stream, const int32_t* tokens, const int32_t* sample_item,

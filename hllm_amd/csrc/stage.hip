@@ -1299,9 +1299,13 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
         gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
              nullptr, 0);
         mark_phase("lm_head", -1);
+        // Without a sampler the argmax also records each sequence's last token (no separate
+        // launch).
         timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
           launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
-                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev());
+                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev(),
+                        sampler ? nullptr : pack_.sample_item, sampler ? nullptr : items_dev_.as<ItemMeta>(),
+                        sampler ? nullptr : last_token_.as<int32_t>());
         });
         if (sampler) {
           HIP_CHECK(hipMemcpyAsync(sample_params_.ptr, pin_sample_params_.ptr, S * sizeof(SampleParams),
@@ -1330,8 +1334,9 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
           HIP_CHECK(hipMemcpyAsync(pin_sample_out_.ptr, sample_out_.ptr, sample_out_.bytes, hipMemcpyDeviceToHost,
                                    stream_));
         }
-        launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
-                             items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
+        if (sampler)
+          launch_record_tokens(stream_, tokens_.as<int32_t>(), pack_.sample_item, pack_.sample_count,
+                               items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
         mark_phase("sampling", -1);
         if (pass.logits)
           HIP_CHECK(hipMemcpyAsync(pass.logits, logits_.ptr, (size_t)S * V_ * sizeof(float),
