@@ -1269,9 +1269,10 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
                                Hp_, Partials{ws, o_parts, (uint64_t)R * H_});
       });
       gemm("gemm_gate_up", w.gate_up, a0h, a0l, R, (int)(2 * Ip_), kEpiSwiglu, nullptr, 0, a1h, a1l, Ip_);
-      // The last layer's residual completes here (the final norm gathers sampled rows, and
-      // the boundary reads the whole stream).
-      const bool defer_down = l + 1 < L_;
+      // The last layer's down partials are summed by the final norm, for the sampled rows it
+      // gathers (nothing reads the other rows' residual afterwards); a boundary stage sums
+      // them here (the boundary reads the whole stream).
+      const bool defer_down = l + 1 < L_ || c_.final_stage;
       const int down_parts = gemm("gemm_down", w.down, a1h, a1l, R, (int)H_, kEpiResidual, h, (int)H_, nullptr,
                                   nullptr, 0, defer_down);
       pending = Partials{ws, down_parts, (uint64_t)R * H_};
@@ -1292,7 +1293,7 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
       if (S > 0) {
         timed("norm", (uint64_t)S * H_ * 6, 0.0, [&] {
           launch_rmsnorm_flayout(stream_, h, (int)H_, pack_.sample_row, S, nullptr, final_norm_.as<float>(), eps,
-                                 a0h, a0l, Hp_);
+                                 a0h, a0l, Hp_, pending);
         });
         mark_phase("final_norm", -1);
         const Matrix& head = c_.tied_head ? embedding_ : head_;
