@@ -100,6 +100,19 @@ __device__ inline float from_half_bits(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
 
+// ------------------------------------------------------------------ greedy argmax
+
+// A candidate of the first-maximum search: larger values win, equal values keep the lower
+// index, NaN never wins (so the result does not depend on the order of the comparisons).
+struct Best {
+  float value;
+  int index;
+};
+__device__ inline Best better(Best a, Best b) {
+  if (b.value > a.value || (b.value == a.value && b.index < a.index)) return b;
+  return a;
+}
+
 // ------------------------------------------------------------------ precision
 
 // How GEMM operands are represented:

@@ -1162,6 +1162,42 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
     }
     return;
   }
+  if (a.epilogue == kEpiArgmax) {
+    // No output: this workgroup's first maximum of every row over its features. The four
+    // lanes of a row combine through shuffles, then the waves in wave order through LDS
+    // (the staged operand is no longer read); the order does not change the result.
+    Best* cand = reinterpret_cast<Best*>(lds);  // [WAVES][16 * MF]
+    __syncthreads();
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const int row = i * 16 + t16;
+      Best b{-INFINITY, 0x7fffffff};
+#pragma unroll
+      for (int n = 0; n < NFW; ++n)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int col = frag[n] * 16 + q4 + t;
+          if (row < M && col < a.N) {
+            const float v = acc[i][n][t];
+            bad |= !isfinite(v);
+            b = better(b, Best{v, col});
+          }
+        }
+      for (int o = 16; o < 64; o <<= 1) b = better(b, Best{__shfl_xor(b.value, o, 64), __shfl_xor(b.index, o, 64)});
+      if (lane < 16) cand[wave * 16 * MF + row] = b;
+    }
+    if (bad) atomicOr(a.argmax_flags, 2);
+    __syncthreads();
+    for (int row = threadIdx.x; row < 16 * MF; row += NT) {
+      if (row >= M) continue;
+      Best b = cand[row];
+      for (int w = 1; w < WAVES; ++w) b = better(b, cand[w * 16 * MF + row]);
+      a.argmax_val[(size_t)row * a.argmax_parts + tile_n] = b.value;
+      a.argmax_idx[(size_t)row * a.argmax_parts + tile_n] = b.index;
+    }
+    return;
+  }
   const bool partial = a.ksplit > 1;  // deferred: a row-major [M][N] matrix per K split
   float* base = partial ? a.workspace + (size_t)split * a.M * a.N : a.out;
   const int ld = partial ? a.N : a.ldo;
@@ -1417,16 +1453,23 @@ bool decode_applies(const GemmArgs& a, int prec, int rows, int cus) {
   return n_tiles * waves >= 4 * cus;
 }
 
+// Fragment rows per wave of the unpaired decode variant: the configured count, halved while
+// the workgroups' tiles would read past the weight rows (padded to 256).
+int decode_frags(const GemmArgs& a, int waves) {
+  const DecodeShape& d = decode_shape(false);
+  int nfw = d.frags >= 4 ? 4 : d.frags >= 2 ? 2 : 1;
+  while (nfw > 1 && (uint64_t)((a.N + 16 * waves * nfw - 1) / (16 * waves * nfw)) * waves * nfw * 16 > a.w_rows_padded)
+    nfw /= 2;
+  return nfw;
+}
+
 template <int MF, int KC, int P>
 int launch_decode_variant(hipStream_t stream, const GemmArgs& a, int cus) {
   const bool pair = a.epilogue == kEpiSwiglu;
   const DecodeShape& d = decode_shape(pair);
   const int chunks = (int)((a.Kp >> 5) + KC - 1) / KC;
   const int waves = d.waves >= 8 ? 8 : 4;
-  int nfw = pair ? 2 : (d.frags >= 4 ? 4 : d.frags >= 2 ? 2 : 1);
-  // Tiles never read past the weight rows (padded to 256).
-  while (nfw > 1 && !pair && (uint64_t)((a.N + 16 * waves * nfw - 1) / (16 * waves * nfw)) * waves * nfw * 16 > a.w_rows_padded)
-    nfw /= 2;
+  const int nfw = pair ? 2 : decode_frags(a, waves);
   const int fr = waves * nfw;
   const int n_tiles = (a.N + 16 * fr - 1) / (16 * fr);
   int ksplit = 1;
@@ -1468,9 +1511,24 @@ std::atomic<int>& forced_config() {
 
 int set_forced_gemm_config(int config) { return forced_config().exchange(config); }
 
+int gemm_argmax_parts(const GemmArgs& a, int prec, int rows_bound, int cus) {
+  if (env_int("HLLM_ROCM_FUSED_ARGMAX", 1) == 0 || a.defer_reduce || a.epilogue == kEpiSwiglu) return 0;
+  const int forced = forced_config().load(std::memory_order_relaxed);
+  if (forced >= 0 || env_int("HLLM_ROCM_DECODE_OFF", 0) != 0 || !decode_applies(a, prec, rows_bound, cus)) return 0;
+  const int waves = decode_shape(false).waves >= 8 ? 8 : 4;
+  const int cols = 16 * waves * decode_frags(a, waves);  // features per workgroup
+  return (a.N + cols - 1) / cols;
+}
+
 int launch_gemm(hipStream_t stream, const GemmArgs& args, int prec, int rows_bound, int cus) {
   if (rows_bound <= 0) return 0;
   const int forced = forced_config().load(std::memory_order_relaxed);
+  if (args.epilogue == kEpiArgmax) {
+    // Only the decode kernel has the argmax epilogue (gemm_argmax_parts says when it runs).
+    if (gemm_argmax_parts(args, prec, rows_bound, cus) != args.argmax_parts || args.argmax_parts <= 0)
+      fail(HLLM_INTERNAL, "the argmax epilogue needs the decode kernel");
+    return launch_decode(stream, args, rows_bound, cus);
+  }
   if (forced < 0 && env_int("HLLM_ROCM_DECODE_OFF", 0) == 0 && decode_applies(args, prec, rows_bound, cus))
     return launch_decode(stream, args, rows_bound, cus);
   if (forced == kDecodeConfig && prec == kF16 && rows_bound <= 64 && (args.defer_reduce || args.epilogue == kEpiSwiglu))

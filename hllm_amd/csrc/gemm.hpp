@@ -9,6 +9,8 @@ enum Epilogue : int {
   kEpiStore = 0,     // out[m][n] = y            (F32 row-major, leading dimension ldo)
   kEpiResidual = 1,  // out[m][n] += y           (the F32 residual stream)
   kEpiSwiglu = 2,    // F-layout act[m][i] = silu(gate) * up, gate/up in 32-wide interleaved groups
+  kEpiArgmax = 3,    // no output: each workgroup's first maximum of every row over its features
+                     // (argmax_val / argmax_idx [m][parts], parts = gemm_argmax_parts)
 };
 
 struct GemmArgs {
@@ -34,6 +36,10 @@ struct GemmArgs {
   uint16_t* out_hi;            // kEpiSwiglu
   uint16_t* out_lo;
   uint64_t out_cols_padded;
+  float* argmax_val;           // kEpiArgmax: [M][argmax_parts] candidates
+  int32_t* argmax_idx;
+  int32_t* argmax_flags;       // bit 1 set when an output is not finite
+  int argmax_parts;
 };
 
 // Activation rows a buffer needs so that every row tile of a launch over up to `rows`
@@ -53,5 +59,9 @@ constexpr int kDecodeConfig = 17;
 // Process-wide override of the configuration choice for every later launch_gemm (-1: the
 // choice by shape; initially HLLM_ROCM_GEMM_CONFIG when set). Returns the previous value.
 int set_forced_gemm_config(int config);
+// The number of per-workgroup argmax candidates per row when launch_gemm can run this
+// projection with the kEpiArgmax epilogue (the decode kernel, one pass over N), else 0;
+// HLLM_ROCM_FUSED_ARGMAX=0, read at every call, says 0 (for tests).
+int gemm_argmax_parts(const GemmArgs& args, int prec, int rows_bound, int cus);
 
 }  // namespace hllm_rocm

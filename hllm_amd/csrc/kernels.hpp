@@ -220,6 +220,11 @@ bool attention_uses_mfma(int head_dim, bool kv_f32);
 
 // Row-wise first maximum over `cols` F32 values per row (greedy sampling) and a
 // non-finite flag (bit 1 of flags).
+// The first maximum of each row over `parts` candidates [rows][parts] (launch_argmax's second
+// kernel, for candidates a GEMM's argmax epilogue wrote).
+void launch_argmax_final(hipStream_t stream, const int32_t* device_rows, int max_rows, int parts,
+                         const float* part_val, const int32_t* part_idx, int32_t* tokens,
+                         const int32_t* sample_item, const ItemMeta* items, int32_t* last_token);
 // With `last_token` set, each row's token is also recorded as its sequence's last token
 // (as launch_record_tokens does: sample_item maps sampled rows to items).
 void launch_argmax(hipStream_t stream, const float* logits, const int32_t* device_rows, int max_rows,

@@ -491,15 +491,6 @@ __global__ void __launch_bounds__(kBlock) qkv_rope_append_kernel(
 
 // ------------------------------------------------------------------ greedy argmax
 
-struct Best {
-  float value;
-  int index;
-};
-__device__ inline Best better(Best a, Best b) {
-  // First maximum: larger value wins; equal values keep the lower index.
-  if (b.value > a.value || (b.value == a.value && b.index < a.index)) return b;
-  return a;
-}
 __device__ inline Best wave_best(Best x) {
   for (int o = 32; o > 0; o >>= 1) {
     Best y{__shfl_xor(x.value, o, 64), __shfl_xor(x.index, o, 64)};
@@ -802,6 +793,16 @@ void launch_argmax(hipStream_t stream, const float* logits, const int32_t* devic
   observed("argmax_partial_kernel", [&] { argmax_partial_kernel<<<dim3(max_rows, parts), kBlock, 0, stream>>>(logits, device_rows, cols,
                                                                       parts, part_val, part_idx,
                                                                       flags); });
+  observed("argmax_final_kernel", [&] {
+    argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens, sample_item, items,
+                                                     last_token);
+  });
+}
+
+void launch_argmax_final(hipStream_t stream, const int32_t* device_rows, int max_rows, int parts,
+                         const float* part_val, const int32_t* part_idx, int32_t* tokens,
+                         const int32_t* sample_item, const ItemMeta* items, int32_t* last_token) {
+  if (max_rows <= 0) return;
   observed("argmax_final_kernel", [&] {
     argmax_final_kernel<<<max_rows, 64, 0, stream>>>(device_rows, parts, part_val, part_idx, tokens, sample_item, items,
                                                      last_token);

@@ -189,10 +189,11 @@ class Stage {
                 uint64_t seed, uint64_t tensor_id, float mean, float sigma, uint64_t row_base,
                 uint64_t rows);
   void read_flags(const char* context);
+  // `argmax_parts` > 0: the kEpiArgmax epilogue into argmax_val_ / argmax_idx_.
   int gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo, int rows,
             int n, int epilogue, float* out, int ldo, uint16_t* out_hi, uint16_t* out_lo,
             uint64_t out_cols_padded,
-           bool defer = false);
+           bool defer = false, int argmax_parts = 0);
   template <typename F>
   void timed(const char* family, uint64_t bytes, double flops, F&& launch);
   hipEvent_t take_event();
@@ -238,6 +239,7 @@ class Stage {
   // Per-pass inputs and outputs share one copy each way: items_dev_ holds the item list, then
   // the input tokens; tokens_ the sampled tokens, then the pass's error flags.
   DeviceMemory gemm_ws_, gemm_counters_, logits_, argmax_val_, argmax_idx_, tokens_;
+  uint64_t argmax_capacity_ = 0;  // entries of argmax_val_ / argmax_idx_
   DeviceMemory items_dev_, pack_buf_, boundary_dev_, staging_, attn_work_;
   bool mfma_attention_ = false;
   uint64_t attn_work_max_ = 0;
@@ -436,8 +438,11 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
   HIP_CHECK(hipMemsetAsync(gemm_counters_.ptr, 0, gemm_counters_.bytes, stream_));
   if (c.final_stage) {
     logits_.allocate(items_max_ * V_ * sizeof(float), "logits");
-    argmax_val_.allocate(items_max_ * kArgmaxParts * sizeof(float), "argmax");
-    argmax_idx_.allocate(items_max_ * kArgmaxParts * sizeof(int32_t), "argmax");
+    // Candidates of the argmax kernels, or of the LM head's argmax epilogue (at most 64 rows,
+    // one candidate per 64 or more features).
+    argmax_capacity_ = std::max<uint64_t>(items_max_ * kArgmaxParts, 64 * ((V_ + 63) / 64));
+    argmax_val_.allocate(argmax_capacity_ * sizeof(float), "argmax");
+    argmax_idx_.allocate(argmax_capacity_ * sizeof(int32_t), "argmax");
     sample_blocks_ = (int)std::min<uint64_t>(items_max_, kSampleBlocks);
     sample_chunks_ = std::max(1, std::min(32, 4 * cus_ / sample_blocks_));
     sample_params_.allocate(items_max_ * sizeof(SampleParams), "sampling");
@@ -1018,7 +1023,7 @@ std::string Stage::profile_records() {
 // consumer and their count is returned (0: the epilogue has been applied).
 int Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const uint16_t* x_lo,
                 int rows, int n, int epilogue, float* out, int ldo, uint16_t* out_hi,
-                uint16_t* out_lo, uint64_t out_cols_padded, bool defer) {
+                uint16_t* out_lo, uint64_t out_cols_padded, bool defer, int argmax_parts) {
   GemmArgs a{};
   a.defer_reduce = defer ? 1 : 0;
   a.w_hi = w.hi.as<uint16_t>();
@@ -1040,10 +1045,17 @@ int Stage::gemm(const char* family, const Matrix& w, const uint16_t* x_hi, const
   a.out_hi = out_hi;
   a.out_lo = out_lo;
   a.out_cols_padded = out_cols_padded;
+  if (argmax_parts > 0) {
+    a.argmax_val = argmax_val_.as<float>();
+    a.argmax_idx = argmax_idx_.as<int32_t>();
+    a.argmax_flags = flags_dev();
+    a.argmax_parts = argmax_parts;
+  }
   const uint64_t wbytes = (uint64_t)n * w.cols_padded * 2 * (w_f32_ ? 2 : 1);
   const uint64_t xbytes = (uint64_t)rows * w.cols_padded * 2 * (x_lo ? 2 : 1);
-  const uint64_t obytes = epilogue == kEpiSwiglu ? (uint64_t)rows * (n / 2) * 2 * (out_lo ? 2 : 1)
-                                                 : (uint64_t)rows * n * 4 * (epilogue == kEpiResidual ? 2 : 1);
+  const uint64_t obytes = epilogue == kEpiArgmax ? 0
+                          : epilogue == kEpiSwiglu ? (uint64_t)rows * (n / 2) * 2 * (out_lo ? 2 : 1)
+                                                   : (uint64_t)rows * n * 4 * (epilogue == kEpiResidual ? 2 : 1);
   const double flops = 2.0 * rows * n * w.cols;
   int parts = 0;
   timed(family, wbytes + xbytes + obytes, flops, [&] { parts = launch_gemm(stream_, a, prec_, rows, cus_); });
@@ -1297,17 +1309,37 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
         });
         mark_phase("final_norm", -1);
         const Matrix& head = c_.tied_head ? embedding_ : head_;
-        gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
-             nullptr, 0);
-        mark_phase("lm_head", -1);
-        // Without a sampler the argmax also records each sequence's last token (no separate
-        // launch).
-        timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
-          launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
-                        argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev(),
-                        sampler ? nullptr : pack_.sample_item, sampler ? nullptr : items_dev_.as<ItemMeta>(),
-                        sampler ? nullptr : last_token_.as<int32_t>());
-        });
+        // Greedy passes that return no logits take each row's first maximum from the LM head's
+        // epilogue (one candidate per workgroup; the logits are never written). Without a
+        // sampler the argmax also records each sequence's last token (no separate launch).
+        GemmArgs probe{};
+        probe.M = S;
+        probe.N = (int)V_;
+        probe.w_rows_padded = head.rows_padded;
+        probe.x_rows_padded = rows_padded_;
+        probe.Kp = head.cols_padded;
+        probe.epilogue = kEpiArgmax;
+        const int fused_parts = sampler || pass.logits ? 0 : gemm_argmax_parts(probe, prec_, S, cus_);
+        if (fused_parts > 0 && (uint64_t)fused_parts * S <= argmax_capacity_) {
+          gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiArgmax, nullptr, 0, nullptr, nullptr, 0, false,
+               fused_parts);
+          mark_phase("lm_head", -1);
+          timed("argmax", 0, 0.0, [&] {
+            launch_argmax_final(stream_, pack_.sample_count, S, fused_parts, argmax_val_.as<float>(),
+                                argmax_idx_.as<int32_t>(), tokens_.as<int32_t>(), pack_.sample_item,
+                                items_dev_.as<ItemMeta>(), last_token_.as<int32_t>());
+          });
+        } else {
+          gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiStore, logits_.as<float>(), (int)V_, nullptr,
+               nullptr, 0);
+          mark_phase("lm_head", -1);
+          timed("argmax", (uint64_t)S * V_ * 4, 0.0, [&] {
+            launch_argmax(stream_, logits_.as<float>(), pack_.sample_count, S, (int)V_, argmax_val_.as<float>(),
+                          argmax_idx_.as<int32_t>(), kArgmaxParts, tokens_.as<int32_t>(), flags_dev(),
+                          sampler ? nullptr : pack_.sample_item, sampler ? nullptr : items_dev_.as<ItemMeta>(),
+                          sampler ? nullptr : last_token_.as<int32_t>());
+          });
+        }
         if (sampler) {
           HIP_CHECK(hipMemcpyAsync(sample_params_.ptr, pin_sample_params_.ptr, S * sizeof(SampleParams),
                                    hipMemcpyHostToDevice, stream_));

@@ -9,6 +9,8 @@ with the full vocabulary, against the F32 CPU oracle:
   gate/up pairs and a SwiGLU register epilogue), and the decode kernel once more with its
   deferred projections staging their activations chunk by chunk instead of whole
   (HLLM_ROCM_DECODE_WHOLE=0: the path for K ranges that do not fit in LDS);
+* the same pass's greedy tokens from the LM head's argmax epilogue (no logits written) and
+  from the argmax kernels over the logits: identical;
 * one pass mixing a 512-token prefill chunk of a new sequence with the same 64 decode rows.
 
 Per row: last-layer hidden state and logits within max-abs 2e-2 and cosine 0.9999."""
@@ -118,6 +120,32 @@ def test_64_decode_rows_with_chunked_activation_staging_match_the_oracle(world):
     hp.greedy_agrees(out["tokens"], w["logits"], out["logits"], "chunked staging")
     for s in seqs:
         st.release(s)
+
+
+def test_lm_head_argmax_epilogue_matches_the_argmax_kernels(world):
+    """Greedy passes that return no logits take each row's first maximum from the LM head's
+    epilogue (per-workgroup candidates, the logits never written): the same tokens as the
+    argmax kernels over the logits, with HLLM_ROCM_FUSED_ARGMAX=0 (read at every pass) and
+    in a pass that returns its logits, and the oracle's tokens up to near ties."""
+    w, st = world, world["stage"]
+    outs = {}
+    for name, want, flag in (("epilogue", False, "1"), ("kernels", False, "0"), ("with logits", True, "1")):
+        hp.say("qwen3-4b 64 decode rows, greedy argmax:", name)
+        seqs = _fresh_sequences(w)
+        before = os.environ.get("HLLM_ROCM_FUSED_ARGMAX")
+        os.environ["HLLM_ROCM_FUSED_ARGMAX"] = flag
+        try:
+            outs[name] = st.execute(_decode_items(seqs, w["lengths"]), token_ids=w["decode_ids"], want_logits=want)
+        finally:
+            if before is None:
+                del os.environ["HLLM_ROCM_FUSED_ARGMAX"]
+            else:
+                os.environ["HLLM_ROCM_FUSED_ARGMAX"] = before
+        for s in seqs:
+            st.release(s)
+    assert np.array_equal(outs["epilogue"]["tokens"], outs["kernels"]["tokens"])
+    assert np.array_equal(outs["epilogue"]["tokens"], outs["with logits"]["tokens"])
+    hp.greedy_agrees(outs["epilogue"]["tokens"], w["logits"], outs["with logits"]["logits"], "argmax epilogue")
 
 
 def test_512_chunk_mixed_with_64_decode_rows_matches_the_oracle(world):
