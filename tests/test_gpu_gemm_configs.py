@@ -2,7 +2,9 @@
 hllm_rocm_set_gemm_config): a ragged pass with a 512-token prefill chunk and decode rows, then
 a decode pass, of a Qwen3-0.6B-shaped two-layer slice in F16 execution, against the F32 CPU
 oracle run per sequence. Covers the configurations that copy both operands into LDS (128-,
-192- and 256-row tiles, four and eight waves), the activation-staged kernel (9), the decode kernel
+192- and 256-row tiles, four and eight waves), the activation-staged kernel (64- and 128-row
+tiles: 12, 9), the register-streaming kernel (16-, 32- and 64-row tiles: 0, 1, 2; the
+choice for plain and F32-execution projections of at most 64 rows), the decode kernel
 (17: the projections it takes in passes of at most 64 rows) and the choice by shape (-1) on
 every epilogue: deferred K-split partials (q/k/v), residual accumulation (o, down), SwiGLU
 (gate+up) and plain stores (LM head), for row counts from 2 to 554. Bounds: max-abs <= 2e-2
@@ -65,7 +67,7 @@ def stage():
     st.close()
 
 
-@pytest.mark.parametrize("config", [-1, 9, 14, 15, 16, 17, 18])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 9, 12, 14, 15, 16, 17, 18])
 def test_forced_configuration_matches_the_oracle(stage, expected, config):
     prompts, first, logits, tokens, second = expected
     _say("gemm configuration", config)
