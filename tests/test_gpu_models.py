@@ -3,9 +3,10 @@ the seeded synthetic Qwen3-0.6B (28 layers) and Qwen3-4B (36 layers), full vocab
 two sequences prefilled in chunks inside shared ragged passes, then decoded together with
 device-fed tokens.
 
-F32 execution must produce the oracle's greedy tokens exactly. F16 execution may only
-depart from them at a step where the oracle's top-two logit margin is within the F16
-tolerance (2e-2 per logit), after which the sequences legitimately diverge."""
+F32 execution must produce the oracle's greedy tokens exactly. F16 execution must produce
+the first LEADING tokens exactly, and may only depart after them at a step where the
+oracle's top-two logit margin is within the F16 tolerance (2e-2 per logit), after which the
+sequences legitimately diverge."""
 import numpy as np
 import pytest
 
@@ -15,6 +16,9 @@ from tests import models
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
+# F16 tokens that must equal the oracle's before any departure at a near tie (these seeded
+# runs measured every token equal: 11 of 11 for Qwen3-0.6B, 5 of 5 for Qwen3-4B).
+LEADING = 4
 # model -> (prompt lengths, prefill chunk, decode steps)
 PLANS = {"qwen3-0.6b": ({"a": 24, "b": 17}, 8, 10), "qwen3-4b": ({"a": 12, "b": 7}, 6, 4)}
 SHAPES = {"qwen3-0.6b": synthetic.QWEN3_0_6B, "qwen3-4b": synthetic.QWEN3_4B}
@@ -79,6 +83,15 @@ def test_f16_greedy_departs_only_at_near_ties(oracle_run):
     got = _gpu_tokens(shape, prompts, chunk, decodes, "f16")
     for k in prompts:
         tokens, logits = ref[k]
+        same = 0
+        for g, r in zip(got[k], tokens):
+            if g != r:
+                break
+            same += 1
+        n = min(len(got[k]), len(tokens))
+        print(f"[gpu-case] {k}: {same} of {n} leading tokens equal", flush=True)
+        # At least the first LEADING tokens (prefill's and the first decode steps') agree.
+        assert same >= min(n, LEADING), (k, same)
         for step, (g, r) in enumerate(zip(got[k], tokens)):
             if g == r:
                 continue
