@@ -1,6 +1,10 @@
 """Builds, in-tree: libhllm_rocm.so (HIP kernels + stage runtime + C ABI, gfx950),
 libhllm_rocm_host.so (the C++ stage-backend adapter, loader and scheduler over that ABI)
-and the host test program tests/host/host_tests.cpp (into _build/host_tests)."""
+and the host test program tests/host/host_tests.cpp (into _build/host_tests).
+
+`python -m hllm_amd.build --sanitize address|thread` builds the host test program with the
+host layer instrumented by ASan + UBSan (g++) or TSan (clang) into _build/host_tests_<kind>;
+tests/test_host.py runs every CPU case under both."""
 from __future__ import annotations
 
 import os
@@ -55,11 +59,21 @@ def build(jobs: int = 4) -> str:
 
 HOST = os.path.join(HERE, "host")
 HOST_LIBRARY = os.path.join(HERE, "libhllm_rocm_host.so")
-HOST_SOURCES = ["json.cpp", "safetensors.cpp", "dense_loader.cpp", "sampling.cpp", "scheduler.cpp",
-                "rocm_stage.cpp"]
+HOST_SOURCES = ["json.cpp", "safetensors.cpp", "dense_loader.cpp", "scheduler.cpp", "rocm_stage.cpp"]
+TEST_DIR = os.path.join(ROOT, "tests", "host")
+# The host test program: its cases, plus the host sampler they check (not part of the library).
+TEST_SOURCES = [os.path.join(TEST_DIR, "host_tests.cpp"), os.path.join(TEST_DIR, "host_sampling.cpp")]
 HOST_TESTS = os.path.join(HERE, "_build", "host_tests")
 CXX = os.environ.get("CXX", "g++")
-CXXFLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}"]
+CXXFLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}",
+            f"-I{TEST_DIR}"]
+# Sanitized host test programs (host code only; the HIP library is linked as built):
+# "address" = ASan + UBSan with g++, "thread" = TSan with clang (GCC 11's TSan reports false
+# double locks around condition_variable::wait_for).
+SANITIZERS = {
+    "address": ("g++", ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined"]),
+    "thread": ("/opt/rocm/llvm/bin/clang++", ["-fsanitize=thread", "-fno-omit-frame-pointer"]),
+}
 
 
 def build_host() -> str:
@@ -71,14 +85,35 @@ def build_host() -> str:
     if r.returncode != 0:
         raise RuntimeError(f"host library build failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, HOST_LIBRARY)
-    tests = os.path.join(ROOT, "tests", "host", "host_tests.cpp")
-    r = subprocess.run([CXX, *CXXFLAGS, "-o", HOST_TESTS + ".tmp", tests, f"-L{HERE}", "-lhllm_rocm_host",
-                        "-lhllm_rocm", f"-Wl,-rpath,$ORIGIN/..", "-pthread"], capture_output=True, text=True)
+    r = subprocess.run([CXX, *CXXFLAGS, "-o", HOST_TESTS + ".tmp", *TEST_SOURCES, f"-L{HERE}", "-lhllm_rocm_host",
+                        "-lhllm_rocm", "-Wl,-rpath,$ORIGIN/..", "-pthread"], capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"host test build failed:\n{r.stdout}\n{r.stderr}")
     os.replace(HOST_TESTS + ".tmp", HOST_TESTS)
     return HOST_LIBRARY
 
 
+def build_sanitized_host_tests(kind: str) -> str:
+    """The host test program with the host layer compiled in and instrumented by `kind`
+    ("address" or "thread"): _build/host_tests_<kind>. Links the built libhllm_rocm.so."""
+    compiler, flags = SANITIZERS[kind]
+    out = os.path.join(HERE, "_build", f"host_tests_{kind}")
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    cxxflags = [f for f in CXXFLAGS if f != "-O2"] + ["-O1", "-g"]
+    srcs = [os.path.join(HOST, s) for s in HOST_SOURCES] + TEST_SOURCES
+    r = subprocess.run([compiler, *cxxflags, *flags, "-o", out + ".tmp", *srcs, f"-L{HERE}", "-lhllm_rocm",
+                        "-Wl,-rpath,$ORIGIN/..", "-pthread"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized host test build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 if __name__ == "__main__":
-    print(build())
+    import argparse
+
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--sanitize", choices=sorted(SANITIZERS),
+                    help="build only the sanitized host test program (after a full build)")
+    ns = ap.parse_args()
+    print(build_sanitized_host_tests(ns.sanitize) if ns.sanitize else build())

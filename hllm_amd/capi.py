@@ -12,7 +12,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libhllm_rocm.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, INVALID_REQUEST, INCOMPATIBLE_WORKER, RESOURCE_EXHAUSTED = 0, 1, 2, 3
 DEADLINE_EXCEEDED, CANCELLED, INTERNAL = 4, 5, 6
@@ -31,7 +31,8 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_stage_profile_records", "hllm_rocm_sample_logits",
            "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config",
            "hllm_rocm_measure_read_bandwidth", "hllm_rocm_stage_execute_profiled",
-           "hllm_rocm_sample_logits_noalloc")
+           "hllm_rocm_sample_logits_noalloc", "hllm_rocm_device_allocator_metrics",
+           "hllm_rocm_device_reset_peak", "hllm_rocm_device_query")
 NOALLOC_MAX_VOCABULARY = 262144
 
 
@@ -64,6 +65,9 @@ class Item(C.Structure):
                 ("generated_index", C.c_uint64)]
 
 
+CancelPoll = C.CFUNCTYPE(C.c_int32, C.c_void_p)
+
+
 class Pass(C.Structure):
     _fields_ = [("items", C.c_uint32), ("item", C.POINTER(Item)),
                 ("token_ids", C.POINTER(C.c_uint64)), ("boundary_in", C.POINTER(C.c_uint16)),
@@ -71,7 +75,18 @@ class Pass(C.Structure):
                 ("logprobs", C.POINTER(C.c_double)), ("top_ids", C.POINTER(C.c_uint64)),
                 ("top_logprobs", C.POINTER(C.c_double)),
                 ("boundary_out", C.POINTER(C.c_uint16)), ("logits", C.POINTER(C.c_float)),
-                ("trace_hidden", C.POINTER(C.c_float))]
+                ("trace_hidden", C.POINTER(C.c_float)), ("cancel_poll", CancelPoll),
+                ("cancel_context", C.c_void_p)]
+
+
+class AllocatorMetrics(C.Structure):
+    _fields_ = [("active_bytes", C.c_uint64), ("cached_bytes", C.c_uint64), ("peak_bytes", C.c_uint64)]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("identity", C.c_char * 40), ("name", C.c_char * 64), ("architecture", C.c_char * 64),
+                ("runtime_version", C.c_int32), ("driver_version", C.c_int32),
+                ("compute_units", C.c_uint32), ("available_bytes", C.c_uint64), ("total_bytes", C.c_uint64)]
 
 
 class PhaseTime(C.Structure):
@@ -135,6 +150,9 @@ def library() -> C.CDLL:
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
     L.hllm_rocm_sample_logits_noalloc.argtypes = L.hllm_rocm_sample_logits.argtypes
+    L.hllm_rocm_device_allocator_metrics.argtypes = [C.c_int32, C.POINTER(AllocatorMetrics)]
+    L.hllm_rocm_device_reset_peak.argtypes = [C.c_int32]
+    L.hllm_rocm_device_query.argtypes = [C.c_int32, C.POINTER(DeviceInfo)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if fn.restype is C.c_int or (fn.restype is None and name != "hllm_rocm_stage_destroy"):
@@ -152,6 +170,24 @@ def check(status: int) -> None:
 
 def _ptr(a, ctype):
     return None if a is None else a.ctypes.data_as(C.POINTER(ctype))
+
+
+def allocator_metrics(device: int = 0) -> dict:
+    """Device memory the library holds on `device` (hllm_rocm_device_allocator_metrics)."""
+    m = AllocatorMetrics()
+    check(library().hllm_rocm_device_allocator_metrics(device, C.byref(m)))
+    return {"active_bytes": m.active_bytes, "cached_bytes": m.cached_bytes, "peak_bytes": m.peak_bytes}
+
+
+def reset_peak(device: int = 0) -> None:
+    check(library().hllm_rocm_device_reset_peak(device))
+
+
+def device_info(device: int = 0) -> dict:
+    d = DeviceInfo()
+    check(library().hllm_rocm_device_query(device, C.byref(d)))
+    return {f: (getattr(d, f).decode() if isinstance(getattr(d, f), bytes) else getattr(d, f))
+            for f, _ in DeviceInfo._fields_}
 
 
 class Stage:
@@ -255,7 +291,9 @@ class Stage:
     # --------------------------------------------------------------- passes
     def make_pass(self, items, token_ids=None, boundary=None, want_logits=False,
                   trace=False, cancelled=None):
-        """Build a Pass (and the output arrays it points at) from a list of Item."""
+        """Build a Pass (and the output arrays it points at) from a list of Item.
+        `cancelled`: an int32 array (the flag), or a Python callable polled through
+        cancel_poll (returns true when the pass is cancelled)."""
         n = len(items)
         arr = (Item * n)(*items)
         rows = sum(int(it.query_tokens) for it in items)
@@ -272,7 +310,11 @@ class Stage:
             b = np.ascontiguousarray(boundary, np.uint16)
             keep["boundary"] = b
             p.boundary_in = _ptr(b, C.c_uint16)
-        if cancelled is not None:
+        if callable(cancelled):
+            poll = CancelPoll(lambda _context: 1 if cancelled() else 0)
+            keep["cancel_poll"] = poll
+            p.cancel_poll = poll
+        elif cancelled is not None:
             keep["cancelled"] = cancelled
             p.cancelled = _ptr(cancelled, C.c_int32)
         out = {"tokens": np.zeros(n, np.uint64)}

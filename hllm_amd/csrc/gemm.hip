@@ -1511,6 +1511,8 @@ std::atomic<int>& forced_config() {
 
 int set_forced_gemm_config(int config) { return forced_config().exchange(config); }
 
+int forced_gemm_config() { return forced_config().load(std::memory_order_relaxed); }
+
 int gemm_argmax_parts(const GemmArgs& a, int prec, int rows_bound, int cus) {
   if (env_int("HLLM_ROCM_FUSED_ARGMAX", 1) == 0 || a.defer_reduce || a.epilogue == kEpiSwiglu) return 0;
   const int forced = forced_config().load(std::memory_order_relaxed);

@@ -59,6 +59,8 @@ constexpr int kDecodeConfig = 17;
 // Process-wide override of the configuration choice for every later launch_gemm (-1: the
 // choice by shape; initially HLLM_ROCM_GEMM_CONFIG when set). Returns the previous value.
 int set_forced_gemm_config(int config);
+// The configuration every projection is forced onto (-1: the choice by shape).
+int forced_gemm_config();
 // The number of per-workgroup argmax candidates per row when launch_gemm can run this
 // projection with the kEpiArgmax epilogue (the decode kernel, one pass over N), else 0;
 // HLLM_ROCM_FUSED_ARGMAX=0, read at every call, says 0 (for tests).

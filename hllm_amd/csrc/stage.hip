@@ -34,30 +34,56 @@ bool rope_fusion_enabled() {
   return on;
 }
 
+// Device memory the library holds, per device (the allocator metrics): bytes held now and
+// the most held at once since the start or the last reset.
+struct Ledger {
+  std::mutex mutex;
+  std::map<int, std::pair<uint64_t, uint64_t>> devices;  // device -> (active, peak)
+  void add(int device, uint64_t n) {
+    std::lock_guard<std::mutex> lock(mutex);
+    auto& [active, peak] = devices[device];
+    active += n;
+    peak = std::max(peak, active);
+  }
+  void remove(int device, uint64_t n) {
+    std::lock_guard<std::mutex> lock(mutex);
+    devices[device].first -= n;
+  }
+};
+Ledger& ledger() {
+  static Ledger* l = new Ledger;  // never destroyed: stages may outlive static destruction
+  return *l;
+}
+
 // Device allocation owned by the stage (RAII: a failed construction frees what it got).
 struct DeviceMemory {
   void* ptr = nullptr;
   size_t bytes = 0;
+  int device = 0;
   DeviceMemory() = default;
   DeviceMemory(const DeviceMemory&) = delete;
   DeviceMemory& operator=(const DeviceMemory&) = delete;
-  ~DeviceMemory() {
-    if (ptr) (void)hipFree(ptr);
-  }
+  ~DeviceMemory() { release(); }
   void release() {
-    if (ptr) (void)hipFree(ptr);
+    if (ptr) {
+      (void)hipFree(ptr);
+      ledger().remove(device, bytes);
+    }
     ptr = nullptr;
     bytes = 0;
   }
   void allocate(size_t n, const char* what) {
     bytes = n;
     if (n == 0) return;
+    HIP_CHECK(hipGetDevice(&device));
     const hipError_t e = hipMalloc(&ptr, n);
     if (e != hipSuccess) {
       ptr = nullptr;
+      bytes = 0;
       fail(HLLM_RESOURCE_EXHAUSTED, std::string("device allocation failed: ") + what + " (" +
                                         std::to_string(n) + " bytes)");
     }
+    ledger().add(device, n);
   }
   template <typename T>
   T* as() const {
@@ -132,6 +158,11 @@ struct Profile {
   double flops = 0.0;
   bool owns_events = true;  // kernel records share the events of their family record
 };
+
+// The pass's cancellation flag or poll (either may be absent).
+bool cancel_requested(const hllm_rocm_pass& pass) {
+  return (pass.cancelled && *pass.cancelled) || (pass.cancel_poll && pass.cancel_poll(pass.cancel_context) != 0);
+}
 
 constexpr int kMaxSplits = 16;
 constexpr int kSplitUnit = 256;
@@ -258,17 +289,20 @@ class Stage {
   PinnedMemory pin_sample_params_, pin_sample_out_;
   int sample_blocks_ = 0, sample_chunks_ = 1;
 
-  // Passes whose shape (items, rows, sampled rows, sampler, attention work items) repeats
-  // can be replayed from a captured HIP graph (off by default: on MI355X the replay saves
-  // no measurable time on these passes, whose kernels, not their launches, set the pace).
-  // Every launch parameter of a pass is a function of its shape (all other per-pass values
-  // are read on the device); a shape is captured the second time it is seen (the first run
-  // sets the kernels' attributes eagerly).
+  // Passes whose shape repeats can be replayed from a captured HIP graph (off by default: on
+  // MI355X the replay saves no measurable time on these passes, whose kernels, not their
+  // launches, set the pace). Every launch parameter of a pass is a function of its shape:
+  // items, rows, sampled rows, sampler, attention work items and splits, and the host-side
+  // choices made per pass (the LM head's argmax-epilogue parts, the forced GEMM
+  // configuration); all other per-pass values are read on the device. A shape is captured
+  // the second time it is seen (the first run sets the kernels' attributes eagerly).
   struct PassShape {
     uint32_t items, rows, samples, sampler, attention_items, any_split;
+    int32_t argmax_parts, gemm_config;
     bool operator<(const PassShape& o) const {
-      return std::tie(items, rows, samples, sampler, attention_items, any_split) <
-             std::tie(o.items, o.rows, o.samples, o.sampler, o.attention_items, o.any_split);
+      return std::tie(items, rows, samples, sampler, attention_items, any_split, argmax_parts, gemm_config) <
+             std::tie(o.items, o.rows, o.samples, o.sampler, o.attention_items, o.any_split, o.argmax_parts,
+                      o.gemm_config);
     }
   };
   struct CapturedPass {
@@ -1146,7 +1180,7 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
     }
     std::memcpy(pin_boundary_.ptr, pass.boundary_in, count * 2);
   }
-  if (pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+  if (cancel_requested(pass)) fail(HLLM_CANCELLED, "request cancelled");
   // Algorithmic attention bytes of one layer: every item's keys and values read once,
   // queries read and outputs written once.
   // FLOPs: 4 * D per (query head, attended key) pair (scores and the value sum).
@@ -1186,6 +1220,22 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
   // One attention workgroup (per KV head) per work item: the hardware's dispatch balances
   // items of different lengths.
   const int attn_grid = attn_work_count;
+  // Greedy passes that return no logits take each row's first maximum from the LM head's
+  // epilogue (one candidate per workgroup; the logits are never written): its part count,
+  // 0 when the logits are written and argmax kernels read them.
+  int fused_parts = 0;
+  if (c_.final_stage && S > 0 && !sampler && !pass.logits) {
+    const Matrix& head = c_.tied_head ? embedding_ : head_;
+    GemmArgs probe{};
+    probe.M = S;
+    probe.N = (int)V_;
+    probe.w_rows_padded = head.rows_padded;
+    probe.x_rows_padded = rows_padded_;
+    probe.Kp = head.cols_padded;
+    probe.epilogue = kEpiArgmax;
+    fused_parts = gemm_argmax_parts(probe, prec_, S, cus_);
+    if ((uint64_t)fused_parts * S > argmax_capacity_) fused_parts = 0;
+  }
   auto enqueue = [&](bool capturing) {
     // The item list (all slots) and, on the first stage, the pass's tokens: one copy.
     HIP_CHECK(hipMemcpyAsync(items_dev_.ptr, meta, tokens_offset() + (c_.first_stage ? R * sizeof(int32_t) : 0),
@@ -1220,7 +1270,7 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
     float* ws = gemm_ws_.as<float>();
     Partials pending{};
     for (uint64_t l = 0; l < L_; ++l) {
-      if (!capturing && pass.cancelled && *pass.cancelled) fail(HLLM_CANCELLED, "request cancelled");
+      if (!capturing && cancel_requested(pass)) fail(HLLM_CANCELLED, "request cancelled");
       Layer& w = *layers_[l];
       timed("norm", (uint64_t)R * H_ * 6, 0.0, [&] {
         launch_rmsnorm_flayout(stream_, h, (int)H_, nullptr, R, nullptr, w.input_norm.as<float>(), eps, a0h, a0l,
@@ -1309,18 +1359,9 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
         });
         mark_phase("final_norm", -1);
         const Matrix& head = c_.tied_head ? embedding_ : head_;
-        // Greedy passes that return no logits take each row's first maximum from the LM head's
-        // epilogue (one candidate per workgroup; the logits are never written). Without a
-        // sampler the argmax also records each sequence's last token (no separate launch).
-        GemmArgs probe{};
-        probe.M = S;
-        probe.N = (int)V_;
-        probe.w_rows_padded = head.rows_padded;
-        probe.x_rows_padded = rows_padded_;
-        probe.Kp = head.cols_padded;
-        probe.epilogue = kEpiArgmax;
-        const int fused_parts = sampler || pass.logits ? 0 : gemm_argmax_parts(probe, prec_, S, cus_);
-        if (fused_parts > 0 && (uint64_t)fused_parts * S <= argmax_capacity_) {
+        // Without a sampler the argmax also records each sequence's last token (no separate
+        // launch).
+        if (fused_parts > 0) {
           gemm("gemm_lm_head", head, a0h, a0l, S, (int)V_, kEpiArgmax, nullptr, 0, nullptr, nullptr, 0, false,
                fused_parts);
           mark_phase("lm_head", -1);
@@ -1415,7 +1456,7 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
   try {
     if (phases) HIP_CHECK(hipEventRecord(phase_start_, stream_));
     const PassShape shape{n, (uint32_t)R, (uint32_t)S, sampler ? 1u : 0u, (uint32_t)attn_grid,
-                          attn_any_split ? 1u : 0u};
+                          attn_any_split ? 1u : 0u, fused_parts, forced_gemm_config()};
     const bool graphable = graphs_enabled_ && !profiling_ && !phases && !pass.logits && !pass.trace_hidden;
     auto found = graphable ? graphs_.find(shape) : graphs_.end();
     if (found != graphs_.end()) {
@@ -1488,7 +1529,7 @@ void Stage::wait(hllm_rocm_phase_time* phases, uint32_t capacity, uint32_t* coun
   // Cancellation is checked before each layer is enqueued and once more when the pass has
   // completed, before the sequences advance (cpp/src/cuda/stage.cpp:396,456): a pass
   // cancelled while it ran is discarded and its sequences are never resumed.
-  if (pending_.cancelled && *pending_.cancelled) {
+  if (cancel_requested(pending_)) {
     fail_pass(pending_sequences_);
     fail(HLLM_CANCELLED, "request cancelled");
   }
@@ -1560,6 +1601,63 @@ void check_sampling(const hllm_rocm_item& it) {
   if (!(it.temperature >= 0.0 && it.temperature <= 100.0) || !(it.top_p > 0.0 && it.top_p <= 1.0) ||
       it.top_logprobs > 5 || (!(it.flags & HLLM_ITEM_LOGPROBS) && it.top_logprobs != 0))
     fail(HLLM_INVALID_REQUEST, "invalid sampling parameters");
+}
+
+hllm_rocm_allocator_metrics allocator_metrics(int32_t device) {
+  int count = 0;
+  HIP_CHECK(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) fail(HLLM_INVALID_REQUEST, "device ordinal out of range");
+  Ledger& l = ledger();
+  std::lock_guard<std::mutex> lock(l.mutex);
+  const auto it = l.devices.find(device);
+  const auto [active, peak] = it == l.devices.end() ? std::pair<uint64_t, uint64_t>{0, 0} : it->second;
+  return {active, 0, peak};
+}
+
+void reset_peak(int32_t device) {
+  int count = 0;
+  HIP_CHECK(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) fail(HLLM_INVALID_REQUEST, "device ordinal out of range");
+  int current = 0;
+  HIP_CHECK(hipGetDevice(&current));
+  HIP_CHECK(hipSetDevice(device));
+  const hipError_t e = hipDeviceSynchronize();
+  (void)hipSetDevice(current);
+  check_hip(e, "device synchronize");
+  Ledger& l = ledger();
+  std::lock_guard<std::mutex> lock(l.mutex);
+  auto& [active, peak] = l.devices[device];
+  peak = active;
+}
+
+hllm_rocm_device_info device_info(int32_t device) {
+  int count = 0;
+  HIP_CHECK(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) fail(HLLM_INVALID_REQUEST, "device ordinal out of range");
+  hipDeviceProp_t p{};
+  HIP_CHECK(hipGetDeviceProperties(&p, device));
+  hllm_rocm_device_info out{};
+  static const char* hex = "0123456789abcdef";
+  for (int i = 0; i < 16; ++i) {
+    const unsigned char b = static_cast<unsigned char>(p.uuid.bytes[i]);
+    out.identity[2 * i] = hex[b >> 4];
+    out.identity[2 * i + 1] = hex[b & 15];
+  }
+  std::strncpy(out.name, p.name, sizeof(out.name) - 1);
+  std::strncpy(out.architecture, p.gcnArchName, sizeof(out.architecture) - 1);
+  HIP_CHECK(hipRuntimeGetVersion(&out.runtime_version));
+  HIP_CHECK(hipDriverGetVersion(&out.driver_version));
+  out.compute_units = (uint32_t)p.multiProcessorCount;
+  int current = 0;
+  HIP_CHECK(hipGetDevice(&current));
+  HIP_CHECK(hipSetDevice(device));
+  size_t free_b = 0, total_b = 0;
+  const hipError_t e = hipMemGetInfo(&free_b, &total_b);
+  (void)hipSetDevice(current);
+  check_hip(e, "memory info");
+  out.available_bytes = free_b;
+  out.total_bytes = total_b;
+  return out;
 }
 
 // Best of five timed streaming reads of `bytes` (after a warm one), in GB/s.
@@ -1854,6 +1952,24 @@ hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled)
 
 hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured, uint64_t* replayed) {
   return guarded([&] { impl(stage).graph_stats(captured, replayed); });
+}
+
+hllm_status hllm_rocm_device_allocator_metrics(int32_t device, hllm_rocm_allocator_metrics* out) {
+  return guarded([&] {
+    if (!out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null output");
+    *out = hllm_rocm::allocator_metrics(device);
+  });
+}
+
+hllm_status hllm_rocm_device_reset_peak(int32_t device) {
+  return guarded([&] { hllm_rocm::reset_peak(device); });
+}
+
+hllm_status hllm_rocm_device_query(int32_t device, hllm_rocm_device_info* out) {
+  return guarded([&] {
+    if (!out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null output");
+    *out = hllm_rocm::device_info(device);
+  });
 }
 
 hllm_status hllm_rocm_measure_read_bandwidth(int32_t device, uint64_t bytes, double* gb_s) {

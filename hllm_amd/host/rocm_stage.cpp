@@ -1,9 +1,21 @@
 #include "rocm_stage.hpp"
 
+#include <cmath>
 #include <cstring>
 #include <limits>
 #include <span>
 #include <unordered_set>
+
+namespace hllm_rocm::runtime {
+
+void validate_sampling(const SamplingOptions& o) {
+  const bool ok = std::isfinite(o.temperature) && o.temperature >= 0.0 && o.temperature <= 100.0 &&
+                  std::isfinite(o.top_p) && o.top_p > 0.0 && o.top_p <= 1.0 && o.top_logprobs <= 5 &&
+                  (o.return_logprobs || o.top_logprobs == 0);
+  if (!ok) throw Error::invalid_request("invalid sampling parameters");
+}
+
+}  // namespace hllm_rocm::runtime
 
 namespace hllm_rocm::backend {
 
@@ -30,7 +42,7 @@ void require_decode_batch(const std::vector<runtime::DecodeBatchItem>& items, st
   for (const runtime::DecodeBatchItem& it : items) {
     if (!it.sequence || !it.cancelled) throw Error::invalid_request("decode batch member without a sequence");
     if (!members.insert(it.sequence).second) throw Error::invalid_request("a sequence is in a decode batch twice");
-    if (it.sequence->prefilling || it.position == 0)
+    if (it.sequence->prefilling || it.sequence->prefill_only || it.position == 0)
       throw Error::invalid_request("decode batch members must be decoding started sequences");
     if (std::holds_alternative<runtime::TokenInput>(it.input) != tokens)
       throw Error::invalid_request("a decode batch mixes token and boundary inputs");
@@ -155,7 +167,13 @@ std::unique_ptr<runtime::SequenceState> RocmStage::allocate_sequence(std::size_t
   return state;
 }
 
-std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, bool batch_outputs) const {
+namespace {
+int32_t poll_cancelled(void* flag) { return static_cast<const std::atomic_bool*>(flag)->load() ? 1 : 0; }
+}  // namespace
+
+std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, bool batch_outputs,
+                                                 const std::atomic_bool* cancelled,
+                                                 runtime::ExecutionTiming* timing) const {
   std::scoped_lock lock(mutex_);
   const std::size_t n = members.size();
   const std::size_t hidden = config_.hidden_size;
@@ -232,9 +250,32 @@ std::vector<runtime::StageOutput> RocmStage::run(std::vector<Member>& members, b
     boundary_out.resize(total_rows * hidden);
     pass.boundary_out = boundary_out.data();
   }
-  const hllm_status status = hllm_rocm_stage_execute(stage_, &pass);
-  if (status == HLLM_INTERNAL)
-    for (RocmSequence* s : states) s->failed = true;  // the pass may have written part of the caches
+  if (cancelled) {
+    pass.cancel_poll = poll_cancelled;
+    pass.cancel_context = const_cast<std::atomic_bool*>(cancelled);
+  }
+  hllm_status status = HLLM_OK;
+  if (timing) {
+    std::vector<hllm_rocm_phase_time> phases(config_.layer_end - config_.layer_start + 8);
+    std::uint32_t count = 0;
+    status = hllm_rocm_stage_execute_profiled(stage_, &pass, phases.data(), static_cast<std::uint32_t>(phases.size()),
+                                              &count);
+    if (status == HLLM_OK) {
+      timing->components.clear();
+      for (std::uint32_t i = 0; i < std::min<std::size_t>(count, phases.size()); ++i) {
+        const hllm_rocm_phase_time& p = phases[i];
+        timing->components.push_back({p.component, p.layer >= 0 ? std::optional<std::size_t>(p.layer) : std::nullopt,
+                                      p.milliseconds});
+      }
+    }
+  } else {
+    status = hllm_rocm_stage_execute(stage_, &pass);
+  }
+  // A pass that failed inside (non-finite values) or was cancelled after it started may
+  // have written part of the caches: its sequences are never resumed
+  // (cpp/src/cuda/stage.cpp:463-468). Cancellation seen before the call throws earlier.
+  if (status == HLLM_INTERNAL || status == HLLM_CANCELLED)
+    for (RocmSequence* s : states) s->failed = true;
   check(status);
 
   std::vector<runtime::StageOutput> out;
@@ -279,7 +320,17 @@ runtime::StageOutput RocmStage::execute(runtime::StageInput input, std::size_t f
                                         runtime::SequenceState& state, const std::atomic_bool& cancelled) const {
   if (cancelled.load()) throw std::runtime_error("request cancelled");
   std::vector<Member> members{{&input, first_position, &state}};
-  auto out = run(members, false);
+  auto out = run(members, false, &cancelled);
+  return std::move(out.front());
+}
+
+runtime::StageOutput RocmStage::execute_profiled(runtime::StageInput input, std::size_t first_position,
+                                                 runtime::SequenceState& state, const std::atomic_bool& cancelled,
+                                                 runtime::ExecutionTiming& timing) const {
+  timing = {};
+  if (cancelled.load()) throw std::runtime_error("request cancelled");
+  std::vector<Member> members{{&input, first_position, &state}};
+  auto out = run(members, false, &cancelled, &timing);
   return std::move(out.front());
 }
 
@@ -312,6 +363,29 @@ BackendCapabilities RocmBackendFactory::capabilities() const {
   c.detail = "hllm-rocm stage worker (gfx950, ABI " + std::to_string(hllm_rocm_abi_version()) + ")";
   c.supports_mixed_precision = true;
   return c;
+}
+
+std::optional<runtime::AllocatorMetrics> RocmBackendFactory::allocator_metrics() const {
+  hllm_rocm_allocator_metrics m{};
+  check(hllm_rocm_device_allocator_metrics(options_.device, &m));
+  return runtime::AllocatorMetrics{m.active_bytes, m.cached_bytes, m.peak_bytes};
+}
+
+bool RocmBackendFactory::profiling_reset_peak() const {
+  check(hllm_rocm_device_reset_peak(options_.device));
+  return true;
+}
+
+runtime::ProfilingDeviceInfo RocmBackendFactory::profiling_device_info() const {
+  hllm_rocm_device_info d{};
+  check(hllm_rocm_device_query(options_.device, &d));
+  auto text = [](const char* s, std::size_t n) { return std::string(s, strnlen(s, n)); };
+  return {text(d.identity, sizeof(d.identity)),
+          text(d.name, sizeof(d.name)) + " (" + text(d.architecture, sizeof(d.architecture)) + ")",
+          "HIP " + std::to_string(d.runtime_version) + ", hllm-rocm ABI " + std::to_string(hllm_rocm_abi_version()),
+          std::to_string(d.driver_version),
+          "hllm-rocm (reserved at stage creation)",
+          static_cast<std::size_t>(d.available_bytes)};
 }
 
 std::unique_ptr<runtime::StageBackend> RocmBackendFactory::load(const model::LoadStageRequest& request,

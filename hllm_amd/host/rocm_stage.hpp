@@ -29,8 +29,8 @@ void check(hllm_status status);
 
 // The decode-batch contract (cpp/include/hllm/runtime/stage_backend.hpp:52-58,93-101): 1..64
 // members, each one row (a token, or a boundary row `hidden` wide) of a distinct sequence that
-// has started and is not prefilling, all with the same kind of input. INVALID_REQUEST
-// otherwise.
+// has started, is not prefilling and is not prefill-only (cpp/src/decode_batch.cpp:8-24), all
+// with the same kind of input. INVALID_REQUEST otherwise.
 void require_decode_batch(const std::vector<runtime::DecodeBatchItem>& items, std::size_t hidden);
 
 class RocmStage final : public runtime::StageBackend, public worker::MixedPassBackend {
@@ -50,8 +50,16 @@ class RocmStage final : public runtime::StageBackend, public worker::MixedPassBa
   runtime::SequenceMemory sequence_memory(std::size_t tokens, std::size_t maximum_query_tokens) const override;
   using runtime::StageBackend::sequence_memory;
   std::unique_ptr<runtime::SequenceState> allocate_sequence(std::size_t tokens) const override;
+  // The pass honours `cancelled` between layers and once more when it completes; a pass
+  // cancelled after it started fails its sequence (never resumed, cpp/src/cuda/stage.cpp:463-468).
   runtime::StageOutput execute(runtime::StageInput input, std::size_t first_position, runtime::SequenceState& state,
                                const std::atomic_bool& cancelled) const override;
+  // execute() with HIP events between phases on the stage's stream: "embedding" or
+  // "from-wire", one "layer" per owned layer, then "final_norm", "lm_head", "sampling" or
+  // "to-wire" (cpp/src/cuda/stage.cpp:234-239). Outputs equal execute()'s bit for bit.
+  runtime::StageOutput execute_profiled(runtime::StageInput input, std::size_t first_position,
+                                        runtime::SequenceState& state, const std::atomic_bool& cancelled,
+                                        runtime::ExecutionTiming& timing) const override;
   bool supports_decode_batch() const override { return true; }
   std::vector<runtime::StageOutput> execute_decode_batch(std::vector<runtime::DecodeBatchItem> items) const override;
 
@@ -68,7 +76,11 @@ class RocmStage final : public runtime::StageBackend, public worker::MixedPassBa
     std::size_t position;
     runtime::SequenceState* state;
   };
-  std::vector<runtime::StageOutput> run(std::vector<Member>& members, bool batch_outputs) const;
+  // `cancelled`: checked inside the pass (single-sequence execution only; batches are not
+  // preempted). `timing`: a profiled pass.
+  std::vector<runtime::StageOutput> run(std::vector<Member>& members, bool batch_outputs,
+                                        const std::atomic_bool* cancelled = nullptr,
+                                        runtime::ExecutionTiming* timing = nullptr) const;
 
   hllm_rocm_stage* stage_{nullptr};
   hllm_rocm_stage_config config_{};
@@ -88,6 +100,13 @@ class RocmBackendFactory {
  public:
   explicit RocmBackendFactory(StageOptions options = {}) : options_(options) {}
   BackendCapabilities capabilities() const;
+  // backend_factory.hpp:31-39: the device memory the library holds on the factory's device
+  // (no caching allocator: cached_bytes 0), boundary rows staged through pinned host memory,
+  // a peak reset after the device's work completes, and the device's identity.
+  std::optional<runtime::AllocatorMetrics> allocator_metrics() const;
+  std::string boundary_transport_mode() const { return "pinned"; }
+  bool profiling_reset_peak() const;
+  runtime::ProfilingDeviceInfo profiling_device_info() const;
   // Validates the request and the memory budget, then returns a complete stage (nothing
   // is published on failure: the partially built stage is destroyed).
   std::unique_ptr<runtime::StageBackend> load(const model::LoadStageRequest& request,

@@ -103,6 +103,16 @@ struct DecodeBatchItem {
   const std::atomic_bool* cancelled;
 };
 
+// timing.hpp:11-18: per-phase times of a profiled execution.
+struct ComponentTiming {
+  std::string component;
+  std::optional<std::size_t> layer_index;
+  double milliseconds;
+};
+struct ExecutionTiming {
+  std::vector<ComponentTiming> components;
+};
+
 // stage_backend.hpp:62-67
 [[nodiscard]] constexpr std::size_t query_rows(std::size_t tokens, std::size_t maximum_query_tokens) noexcept {
   return maximum_query_tokens == 0 || maximum_query_tokens > tokens ? tokens : maximum_query_tokens;
@@ -132,15 +142,29 @@ class StageBackend {
       outputs.push_back(execute(std::move(item.input), item.position, *item.sequence, *item.cancelled));
     return outputs;
   }
+  // Diagnostics for profiling processes (stage_backend.hpp:102-106); serving uses execute().
+  [[nodiscard]] virtual StageOutput execute_profiled(StageInput, std::size_t, SequenceState&,
+                                                     const std::atomic_bool&, ExecutionTiming&) const {
+    throw std::logic_error("backend does not implement compute profiling");
+  }
 };
 
-// sampling.cpp:10-89 restated on the host, for callers that hold logits in host memory.
-// Stage passes sample on the device (hllm_rocm_stage_execute; hllm_rocm_sample_logits for
-// other logits), with the same options and counter.
+// backend_factory.hpp:24-26 and profiling.hpp:8-15: the factory's allocator and device
+// diagnostics.
+struct AllocatorMetrics {
+  std::size_t active_bytes, cached_bytes, peak_bytes;
+};
+struct ProfilingDeviceInfo {
+  std::string identity;
+  std::string name;
+  std::string backend_version;
+  std::string driver_version;
+  std::string allocator;
+  std::optional<std::size_t> available_bytes;
+};
+
+// cpp/src/sampling.cpp:10-17: the options every sampled pass is checked against
+// (INVALID_REQUEST otherwise). Stage passes sample on the device.
 void validate_sampling(const SamplingOptions& options);
-std::uint64_t sample_logits(const float* logits, std::size_t count, const SamplingOptions& options,
-                            std::uint64_t generated_index);
-SampledToken sample_token(const float* logits, std::size_t count, const SamplingOptions& options,
-                          std::uint64_t generated_index);
 
 }  // namespace hllm_rocm::runtime

@@ -32,6 +32,9 @@ std::size_t input_rows(const runtime::StageInput& input) {
 
 StageScheduler::StageScheduler() : dispatcher_([this] { dispatch_loop(); }) {}
 
+// Shutdown: the running pass (if any) completes and delivers its results; requests still
+// queued fail CANCELLED; destruction waits until every caller has left execute(), so no
+// caller touches the scheduler's lock or condition variables after it is gone.
 StageScheduler::~StageScheduler() {
   {
     std::scoped_lock lock(mutex_);
@@ -39,6 +42,8 @@ StageScheduler::~StageScheduler() {
   }
   work_.notify_all();
   dispatcher_.join();
+  std::unique_lock lock(mutex_);
+  done_.wait(lock, [&] { return callers_ == 0; });
 }
 
 void StageScheduler::configure(const PassPolicy& policy) {
@@ -84,12 +89,24 @@ runtime::StageOutput StageScheduler::execute(const runtime::StageBackend& backen
   r.backend = &backend;
   r.rows = input_rows(input);
   if (r.rows == 0) throw Error::invalid_request("empty stage input");
-  r.decode = r.rows == 1 && !sequence.prefilling;
+  // A decode continues a started sequence (cpp/src/worker/scheduler.cpp:48 classes position 0
+  // and prefilling sequences as prefills); prefill-only sequences never join decode batches
+  // (cpp/src/decode_batch.cpp:16-17).
+  r.decode = r.rows == 1 && position != 0 && !sequence.prefilling && !sequence.prefill_only;
   r.item = runtime::DecodeBatchItem{std::move(input), position, &sequence, &cancelled};
   r.deadline = deadline;
   r.queued = Clock::now();
   std::unique_lock lock(mutex_);
   if (stopping_) throw Error::cancelled("the stage is shutting down");
+  // Leaves under the lock (declared after it, destroyed before it): the destructor waits
+  // for the last caller.
+  struct Caller {
+    StageScheduler& s;
+    explicit Caller(StageScheduler& scheduler) : s(scheduler) { ++s.callers_; }
+    ~Caller() {
+      if (--s.callers_ == 0) s.done_.notify_all();
+    }
+  } caller(*this);
   (r.decode ? decode_queue_ : prefill_queue_).push_back(&r);
   work_.notify_one();
   // A queued request watches its own cancellation and deadline; once claimed it belongs to
@@ -205,7 +222,17 @@ void StageScheduler::dispatch_loop() {
   std::unique_lock lock(mutex_);
   for (;;) {
     work_.wait(lock, [&] { return stopping_ || (!held_ && (!prefill_queue_.empty() || !decode_queue_.empty())); });
-    if (stopping_) return;
+    if (stopping_) {
+      for (auto* queue : {&prefill_queue_, &decode_queue_}) {
+        for (Request* r : *queue) {
+          r->failure = std::make_exception_ptr(Error::cancelled("the stage is shutting down"));
+          r->finished = true;
+        }
+        queue->clear();
+      }
+      done_.notify_all();
+      return;
+    }
     if (retire_unready()) done_.notify_all();
     bool mixed = false;
     const std::vector<Request*> pass = plan(mixed);

@@ -16,7 +16,9 @@
 // Guarantees kept from the reference: arrival order within each queue; neither queue starves
 // the other; a request cancelled or past its deadline before dispatch never reaches the
 // backend (CANCELLED / DEADLINE_EXCEEDED); a request whose pass is running gets that pass's
-// result or failure, whatever happens to its cancellation flag meanwhile.
+// result or failure, whatever happens to its cancellation flag meanwhile. Destroying the
+// scheduler lets a running pass finish, fails the queued requests CANCELLED and returns
+// once every caller has left execute().
 #pragma once
 
 #include <atomic>
@@ -104,6 +106,7 @@ class StageScheduler final {
   Kind last_kind_{Kind::kNone};
   SchedulerMetrics totals_{};
   std::size_t executing_{0};
+  std::size_t callers_{0};  // threads inside execute()
   std::thread dispatcher_;
 };
 

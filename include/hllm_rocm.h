@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLLM_ROCM_ABI_VERSION 1u
+#define HLLM_ROCM_ABI_VERSION 2u
 
 /* runtime::ErrorCode (cpp/include/hllm/runtime/error.hpp:10-17), numbered from 1. */
 typedef enum {
@@ -116,6 +116,12 @@ typedef struct {
   uint16_t* boundary_out;        /* non-final: [sum(query_tokens), hidden] F16 LE */
   float* logits;                 /* final: [sampled items, vocabulary] F32, for tests */
   float* trace_hidden;           /* [owned layers, sum(query_tokens), hidden] F32, for tests */
+  /* Optional, read at the same points as `cancelled`: cancel_poll(cancel_context) != 0 means
+   * the pass is cancelled. For callers whose flag is not an int32_t (the reference's
+   * `const std::atomic_bool& cancelled` of StageBackend::execute, stage_backend.hpp:86-89).
+   * The context must stay valid until the pass's execute or wait call returns. */
+  int32_t (*cancel_poll)(void* cancel_context);
+  void* cancel_context;
 } hllm_rocm_pass;
 
 typedef struct {
@@ -124,6 +130,30 @@ typedef struct {
   uint64_t pinned_host_bytes;
   uint64_t unified_bytes;
 } hllm_rocm_memory;  /* runtime::MemoryAmounts (cpp/include/hllm/runtime/memory.hpp:11-17) */
+
+/* BackendFactory::allocator_metrics (cpp/include/hllm/runtime/backend_factory.hpp:24-33):
+ * device memory this library holds on `device`. Stages reserve every buffer when they are
+ * created, straight from hipMalloc with no caching layer, so cached_bytes is always 0;
+ * peak_bytes is the most held at once since the process started or the last reset. */
+typedef struct {
+  uint64_t active_bytes;
+  uint64_t cached_bytes;
+  uint64_t peak_bytes;
+} hllm_rocm_allocator_metrics;
+
+/* BackendFactory::profiling_device_info (cpp/include/hllm/runtime/profiling.hpp:8-15; the CUDA
+ * worker's cpp/src/cuda/device.cpp:93-108): the device's identity (UUID, hex), product name,
+ * ISA, HIP runtime and driver versions, compute units and free / total HBM. */
+typedef struct {
+  char identity[40];
+  char name[64];
+  char architecture[64];
+  int32_t runtime_version;
+  int32_t driver_version;
+  uint32_t compute_units;
+  uint64_t available_bytes;
+  uint64_t total_bytes;
+} hllm_rocm_device_info;
 
 /* Thread-local message of the last failed call on this thread. */
 const char* hllm_rocm_last_error(void);
@@ -237,6 +267,13 @@ hllm_status hllm_rocm_sample_logits_noalloc(int32_t device, const float* logits,
 hllm_status hllm_rocm_stage_set_graphs(hllm_rocm_stage* stage, uint32_t enabled);
 hllm_status hllm_rocm_stage_graph_stats(hllm_rocm_stage* stage, uint64_t* captured,
                                         uint64_t* replayed);
+
+/* BackendFactory::allocator_metrics / profiling_reset_peak / profiling_device_info
+ * (cpp/include/hllm/runtime/backend_factory.hpp:31-39; cpp/src/cuda/device.cpp:41-54,84-108).
+ * reset_peak waits for the device's work to complete, then sets the peak to the bytes held. */
+hllm_status hllm_rocm_device_allocator_metrics(int32_t device, hllm_rocm_allocator_metrics* out);
+hllm_status hllm_rocm_device_reset_peak(int32_t device);
+hllm_status hllm_rocm_device_query(int32_t device, hllm_rocm_device_info* out);
 
 /* Diagnostics: the HBM read ceiling of `device`, measured as the best of five streaming
  * reads of `bytes` (at least 1 MiB, a multiple of 16) with a plain read kernel, in GB/s.

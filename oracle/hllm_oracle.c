@@ -165,6 +165,28 @@ static void parallel_elements(size_t count, void (*body)(void*, size_t, size_t),
   for (int t = 1; t < threads; ++t) pthread_join(ids[t], NULL);
 }
 
+/* body(context, begin, end) over [0, count) units in contiguous ranges, one per thread
+ * (for units that each carry much work). */
+static void parallel_units(size_t count, void (*body)(void*, size_t, size_t), void* context) {
+  int threads = thread_count();
+  if ((size_t)threads > count) threads = (int)count;
+  if (threads > 64) threads = 64;
+  if (threads <= 1) {
+    body(context, 0, count);
+    return;
+  }
+  element_job jobs[64];
+  pthread_t ids[64];
+  const size_t per = (count + (size_t)threads - 1) / (size_t)threads;
+  for (int t = 0; t < threads; ++t) {
+    const size_t b = (size_t)t * per;
+    jobs[t] = (element_job){body, context, b < count ? b : count, b + per < count ? b + per : count};
+  }
+  for (int t = 1; t < threads; ++t) pthread_create(&ids[t], NULL, element_worker, &jobs[t]);
+  element_worker(&jobs[0]);
+  for (int t = 1; t < threads; ++t) pthread_join(ids[t], NULL);
+}
+
 /* cpp/src/cpu/llama.cpp:193-212: y = (x * inv_rms) * w, sequential F32 square sum. */
 void orc_rms_norm(const float* input, size_t rows, size_t columns, const float* weights,
                   float epsilon, float* output) {
@@ -186,34 +208,63 @@ typedef struct {
   size_t first_output, last_output;
 } linear_job;
 
-/* Four output columns at a time for instruction-level parallelism; each sum is still
- * the reference's sequential `sum += x * w` over the inner index. */
+typedef float v4sf __attribute__((vector_size(16)));
+
+/* Eight output columns and two rows at a time: the eight weight rows are interleaved into
+ * [k][8] once per block, and each lane of the four-wide vectors carries one (row, column)
+ * sum. Every sum is still the reference's sequential `sum += x * w` over the inner index
+ * (one multiplication, then one addition, per lane and step; no fused multiply-add). */
 static void* linear_worker(void* opaque) {
   const linear_job* job = (const linear_job*)opaque;
   const size_t n = job->inner;
   size_t o = job->first_output;
-  for (; o + 4 <= job->last_output; o += 4) {
-    const float* w0 = job->weights + o * n;
-    const float* w1 = w0 + n;
-    const float* w2 = w1 + n;
-    const float* w3 = w2 + n;
-    for (size_t r = 0; r < job->rows; ++r) {
-      const float* x = job->input + r * n;
-      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  v4sf* block = (v4sf*)aligned_alloc(16, n * 2 * sizeof(v4sf) + 16);
+  for (; o + 8 <= job->last_output; o += 8) {
+    for (size_t k = 0; k < n; ++k) {
+      for (int c = 0; c < 4; ++c) {
+        block[2 * k][c] = job->weights[(o + (size_t)c) * n + k];
+        block[2 * k + 1][c] = job->weights[(o + 4 + (size_t)c) * n + k];
+      }
+    }
+    size_t r = 0;
+    for (; r + 2 <= job->rows; r += 2) {
+      const float* x0 = job->input + r * n;
+      const float* x1 = x0 + n;
+      v4sf a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
       for (size_t k = 0; k < n; ++k) {
-        const float v = x[k];
-        s0 += v * w0[k];
-        s1 += v * w1[k];
-        s2 += v * w2[k];
-        s3 += v * w3[k];
+        const v4sf w0 = block[2 * k], w1 = block[2 * k + 1];
+        const v4sf u = {x0[k], x0[k], x0[k], x0[k]};
+        const v4sf v = {x1[k], x1[k], x1[k], x1[k]};
+        a0 += u * w0;
+        a1 += u * w1;
+        b0 += v * w0;
+        b1 += v * w1;
+      }
+      float* y0 = job->output + r * job->outputs + o;
+      float* y1 = y0 + job->outputs;
+      for (int c = 0; c < 4; ++c) {
+        y0[c] = a0[c];
+        y0[4 + c] = a1[c];
+        y1[c] = b0[c];
+        y1[4 + c] = b1[c];
+      }
+    }
+    for (; r < job->rows; ++r) {
+      const float* x = job->input + r * n;
+      v4sf a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+      for (size_t k = 0; k < n; ++k) {
+        const v4sf u = {x[k], x[k], x[k], x[k]};
+        a0 += u * block[2 * k];
+        a1 += u * block[2 * k + 1];
       }
       float* y = job->output + r * job->outputs + o;
-      y[0] = s0;
-      y[1] = s1;
-      y[2] = s2;
-      y[3] = s3;
+      for (int c = 0; c < 4; ++c) {
+        y[c] = a0[c];
+        y[4 + c] = a1[c];
+      }
     }
   }
+  free(block);
   for (; o < job->last_output; ++o) {
     const float* w = job->weights + o * n;
     for (size_t r = 0; r < job->rows; ++r) {
@@ -232,11 +283,11 @@ void orc_linear(const float* input, size_t rows, size_t inner, const float* weig
   int threads = thread_count();
   const double work = (double)rows * (double)inner * (double)outputs;
   if (work < 4.0e6 || outputs < 64) threads = 1;
-  if ((size_t)threads > outputs / 4) threads = (int)(outputs / 4 > 0 ? outputs / 4 : 1);
+  if ((size_t)threads > outputs / 8) threads = (int)(outputs / 8 > 0 ? outputs / 8 : 1);
   linear_job jobs[64];
   pthread_t ids[64];
   if (threads > 64) threads = 64;
-  const size_t per = ((outputs + (size_t)threads - 1) / (size_t)threads + 3) / 4 * 4;
+  const size_t per = ((outputs + (size_t)threads - 1) / (size_t)threads + 7) / 8 * 8;
   int launched = 0;
   for (int t = 0; t < threads; ++t) {
     size_t first = (size_t)t * per;
@@ -329,46 +380,77 @@ int orc_kv_append(orc_kv_cache* cache, size_t first_position, const float* keys,
   return ORC_OK;
 }
 
-/* cpp/src/cpu/llama.cpp:67-112: causal GQA attention over the whole cache prefix;
- * probabilities are divided by the denominator inside the value sum. */
-void orc_attention(const float* queries, size_t rows, const orc_config* config,
-                   size_t first_position, const orc_kv_cache* cache, float* output) {
+typedef struct {
+  const float* queries;
+  size_t rows;
+  const orc_config* config;
+  size_t first_position;
+  const orc_kv_cache* cache;
+  float* output;
+} attention_job;
+
+/* Attention of (row, query head) units [begin, end). Each unit's arithmetic is the
+ * reference's: scores in key order, the running maximum, exp and the denominator in key
+ * order, then every output dimension's sum over keys in key order with the probability
+ * divided by the denominator inside the sum. The value loop visits keys in the outer loop
+ * (every dimension's partial sum advances one key at a time), which keeps each dimension's
+ * additions in the same order. */
+static void attention_units(void* context, size_t begin, size_t end) {
+  const attention_job* job = (const attention_job*)context;
+  const orc_config* config = job->config;
   const size_t D = config->head_dimension;
   const size_t K = config->key_value_heads;
-  const size_t group = config->attention_heads / K;
-  const size_t width = config->attention_heads * D;
+  const size_t Q = config->attention_heads;
+  const size_t group = Q / K;
+  const size_t width = Q * D;
   const float scale = 1.0f / sqrtf((float)D);
-  float* scores = (float*)malloc((first_position + rows) * sizeof(float));
-  for (size_t t = 0; t < rows; ++t) {
-    const size_t last = first_position + t - (orc_planted_mistake == 3 && first_position + t > 0);
-    for (size_t qh = 0; qh < config->attention_heads; ++qh) {
-      const size_t kvh = qh / group;
-      const float* q = queries + t * width + qh * D;
-      float maximum = -INFINITY;
-      for (size_t p = 0; p <= last; ++p) {
-        const float* k = cache->keys + (p * K + kvh) * D;
-        float score = 0.0f;
-        for (size_t d = 0; d < D; ++d) score += q[d] * k[d];
-        score *= scale;
-        scores[p] = score;
-        if (maximum < score) maximum = score;
-      }
-      float denominator = 0.0f;
-      for (size_t p = 0; p <= last; ++p) {
-        scores[p] = expf(scores[p] - maximum);
-        denominator += scores[p];
-      }
-      float* out = output + t * width + qh * D;
-      for (size_t d = 0; d < D; ++d) {
-        float sum = 0.0f;
-        for (size_t p = 0; p <= last; ++p) {
-          sum += (scores[p] / denominator) * cache->values[(p * K + kvh) * D + d];
-        }
-        out[d] = sum;
-      }
+  float* scores = (float*)malloc((job->first_position + job->rows) * sizeof(float));
+  float* sums = (float*)malloc(D * sizeof(float));
+  for (size_t unit = begin; unit < end; ++unit) {
+    const size_t t = unit / Q, qh = unit % Q;
+    const size_t last = job->first_position + t - (orc_planted_mistake == 3 && job->first_position + t > 0);
+    const size_t kvh = qh / group;
+    const float* q = job->queries + t * width + qh * D;
+    float maximum = -INFINITY;
+    for (size_t p = 0; p <= last; ++p) {
+      const float* k = job->cache->keys + (p * K + kvh) * D;
+      float score = 0.0f;
+      for (size_t d = 0; d < D; ++d) score += q[d] * k[d];
+      score *= scale;
+      scores[p] = score;
+      if (maximum < score) maximum = score;
     }
+    float denominator = 0.0f;
+    for (size_t p = 0; p <= last; ++p) {
+      scores[p] = expf(scores[p] - maximum);
+      denominator += scores[p];
+    }
+    for (size_t d = 0; d < D; ++d) sums[d] = 0.0f;
+    for (size_t p = 0; p <= last; ++p) {
+      const float weight = scores[p] / denominator;
+      const float* v = job->cache->values + (p * K + kvh) * D;
+      for (size_t d = 0; d < D; ++d) sums[d] += weight * v[d];
+    }
+    float* out = job->output + t * width + qh * D;
+    for (size_t d = 0; d < D; ++d) out[d] = sums[d];
   }
+  free(sums);
   free(scores);
+}
+
+/* cpp/src/cpu/llama.cpp:67-112: causal GQA attention over the whole cache prefix;
+ * probabilities are divided by the denominator inside the value sum. Units of (row, query
+ * head) are independent, so they are spread over threads without changing any result. */
+void orc_attention(const float* queries, size_t rows, const orc_config* config,
+                   size_t first_position, const orc_kv_cache* cache, float* output) {
+  attention_job job = {queries, rows, config, first_position, cache, output};
+  const size_t units = rows * config->attention_heads;
+  const double work = (double)units * (double)(first_position + rows) * (double)config->head_dimension;
+  if (work < 4.0e6) {
+    attention_units(&job, 0, units);
+    return;
+  }
+  parallel_units(units, attention_units, &job);
 }
 
 /* cpp/src/cpu/llama.cpp:242-282: norm -> q,k,v -> QK-norm -> RoPE -> append ->

@@ -1,20 +1,16 @@
-// Host sampling of the stage contract (cpp/src/sampling.cpp:10-89): temperature in double
-// precision, candidates sorted by probability (ties by lower token ID), top-k, then the
-// smallest prefix whose mass reaches top_p of the total, and a SplitMix64 counter draw
-// (seed + golden-ratio increment * (generated_index + 1)) scaled to the retained mass.
+// Host restatement of the reference's sampler (cpp/src/sampling.cpp:19-89) for the host
+// tests: temperature in double precision, candidates sorted by probability (ties by lower
+// token ID), top-k, then the smallest prefix whose mass reaches top_p of the total, and a
+// SplitMix64 counter draw (seed + golden-ratio increment * (generated_index + 1)) scaled to
+// the retained mass. The product samples on the device (hllm_amd/csrc/sampling.hip); this
+// file is built into the host test program only, which checks it against the sampling
+// vectors the device sampler is also checked against.
+#include "host_sampling.hpp"
+
 #include <algorithm>
 #include <cmath>
 
-#include "runtime.hpp"
-
 namespace hllm_rocm::runtime {
-
-void validate_sampling(const SamplingOptions& o) {
-  const bool ok = std::isfinite(o.temperature) && o.temperature >= 0.0 && o.temperature <= 100.0 &&
-                  std::isfinite(o.top_p) && o.top_p > 0.0 && o.top_p <= 1.0 && o.top_logprobs <= 5 &&
-                  (o.return_logprobs || o.top_logprobs == 0);
-  if (!ok) throw Error::invalid_request("invalid sampling parameters");
-}
 
 namespace {
 // Finalizer of Vigna's SplitMix64 applied to the request's counter.

@@ -12,10 +12,13 @@
 #include <functional>
 #include <future>
 #include <map>
+#include <memory>
+#include <optional>
 #include <sstream>
 #include <thread>
 
 #include "dense_loader.hpp"
+#include "host_sampling.hpp"
 #include "json.hpp"
 #include "rocm_stage.hpp"
 #include "runtime.hpp"
@@ -304,6 +307,10 @@ void decode_batch_rules() {
   EXPECT_ERROR(backend::require_decode_batch(Items{}, 6), kInvalidRequest);
   EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 0, &a, &stop}}, 6), kInvalidRequest);  // not started
   EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &busy, &stop}}, 6), kInvalidRequest);
+  runtime::SequenceState only;
+  only.prefill_only = true;
+  EXPECT_ERROR(backend::require_decode_batch(Items{{tok(5), 3, &a, &stop}, {tok(1), 2, &only, &stop}}, 6),
+               kInvalidRequest);
   EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &a, &stop}, {tok(2), 2, &a, &stop}}, 6),
                kInvalidRequest);
   EXPECT_ERROR(backend::require_decode_batch(Items{{tok(1), 2, &a, &stop}, {row(6), 2, &b, &stop}}, 6),
@@ -436,10 +443,14 @@ struct Callers {
   std::deque<std::atomic_bool> flags;
   std::vector<std::future<runtime::StageOutput>> results;
   // Queues one request (ids: its token IDs, first = its name) and waits until it is queued.
+  // `position` defaults to 0 for prompts and 1 for single tokens.
   std::size_t submit(std::vector<std::uint64_t> ids, bool prefill,
-                      std::chrono::milliseconds deadline = std::chrono::milliseconds(5000)) {
+                      std::chrono::milliseconds deadline = std::chrono::milliseconds(5000),
+                      std::optional<std::size_t> position = std::nullopt, bool prefill_only = false) {
     sequences.emplace_back();
     sequences.back().prefilling = prefill;
+    sequences.back().prefill_only = prefill_only;
+    const std::size_t at = position ? *position : prefill_position(ids);
     flags.emplace_back(false);
     runtime::SequenceState& s = sequences.back();
     std::atomic_bool& stop = flags.back();
@@ -449,8 +460,8 @@ struct Callers {
       return m.queued_prefills + m.queued_decodes + m.executing + m.completed_steps;
     };
     const std::size_t queued = seen();
-    results.push_back(std::async(std::launch::async, [this, ids, &s, &stop, deadline] {
-      return scheduler.execute(backend, runtime::TokenInput{ids}, prefill_position(ids), s, stop,
+    results.push_back(std::async(std::launch::async, [this, ids, &s, &stop, deadline, at] {
+      return scheduler.execute(backend, runtime::TokenInput{ids}, at, s, stop,
                                std::chrono::system_clock::now() + deadline);
     }));
     CHECK(wait_for([&] { return seen() > queued; }));
@@ -588,6 +599,55 @@ void scheduler_without_mixed_passes(bool batches) {
   CHECK(scheduler.metrics().mixed_passes == 0);
 }
 
+// A one-token request at position 0 starts its sequence and a prefill-only sequence never
+// decodes: both are prefills (cpp/src/worker/scheduler.cpp:48; cpp/src/decode_batch.cpp:16-17),
+// so neither joins a decode batch and fails its healthy members.
+void scheduler_classifies_first_tokens_as_prefills() {
+  worker::StageScheduler scheduler;
+  scheduler.configure(worker::PassPolicy{8, 512});
+  RecordingStage stage;
+  stage.open.set_value();
+  Callers c{scheduler, stage, {}, {}, {}};
+  scheduler.hold();
+  c.submit({1}, false);
+  c.submit({50}, false, std::chrono::milliseconds(5000), 0);         // position 0
+  c.submit({2}, false);
+  c.submit({60}, false, std::chrono::milliseconds(5000), 7, true);   // prefill-only
+  CHECK(scheduler.metrics().queued_decodes == 2 && scheduler.metrics().queued_prefills == 2);
+  scheduler.resume();
+  for (std::size_t i = 0; i < 4; ++i) static_cast<void>(c.results[i].get());
+  using P = std::vector<std::vector<std::uint64_t>>;
+  CHECK(stage.passes == (P{{1, 2}, {50}, {60}}));
+}
+
+// Destroying the scheduler: the running pass delivers its result, queued requests fail
+// CANCELLED, and the destructor returns only once every caller has left execute().
+void scheduler_shutdown(bool running) {
+  MixedRecordingStage stage;
+  auto scheduler = std::make_unique<worker::StageScheduler>();
+  Callers c{*scheduler, stage, {}, {}, {}};
+  std::size_t gate = 0;
+  if (running) {
+    gate = c.submit({999}, false);  // holds the dispatcher inside its pass
+    CHECK(wait_for([&] { return scheduler->metrics().executing == 1; }));
+  } else {
+    scheduler->hold();
+  }
+  const std::size_t decode = c.submit({1}, false);
+  const std::size_t prefill = c.submit(prefill_ids(100, 3), true);
+  std::thread opener([&] {
+    std::this_thread::sleep_for(50ms);
+    stage.open.set_value();
+  });
+  scheduler.reset();
+  opener.join();
+  if (running) CHECK(c.token(gate) == 999);
+  EXPECT_ERROR(c.results[decode].get(), kCancelled);
+  EXPECT_ERROR(c.results[prefill].get(), kCancelled);
+  using P = std::vector<std::vector<std::uint64_t>>;
+  CHECK(stage.passes == (running ? P{{999}} : P{}));
+}
+
 void scheduler_configuration() {
   worker::StageScheduler s;
   EXPECT_ERROR(s.configure(worker::PassPolicy{0, 512}), kInvalidRequest);
@@ -602,9 +662,12 @@ void scheduler_configuration() {
 // ------------------------------------------------------------------ GPU: the adapter
 
 // Loads a checkpoint directory through the factory and runs a greedy prefill then
-// `decodes` decode steps; prints the sampled tokens as a JSON list.
+// `decodes` decode steps; prints the sampled tokens as a JSON list. With a fifth argument
+// "logprobs", every step also returns the five best log-probabilities, printed per step as
+// "TOP [[id, logprob], ...]".
 void gpu_checkpoint_greedy(const std::vector<std::string>& args) {
-  CHECK(args.size() == 4);
+  CHECK(args.size() == 4 || (args.size() == 5 && args[4] == "logprobs"));
+  const bool logprobs = args.size() == 5;
   const fs::path dir = args[0];
   const std::string dtype = args[1];
   std::vector<std::uint64_t> prompt;
@@ -627,13 +690,22 @@ void gpu_checkpoint_greedy(const std::vector<std::string>& args) {
   auto stage = factory.load(r, dir, capacity);
   std::atomic_bool stop{false};
   auto seq = stage->allocate_sequence(prompt.size() + decodes + 1);
+  if (logprobs) seq->sampling = {0.0, 1.0, 0, 0, true, 5};
   std::vector<std::uint64_t> out;
-  auto t = std::get<runtime::SampledToken>(stage->execute(runtime::TokenInput{prompt}, 0, *seq, stop)).id;
-  out.push_back(t);
-  for (int i = 0; i < decodes; ++i) {
-    t = std::get<runtime::SampledToken>(stage->execute(runtime::TokenInput{{t}}, prompt.size() + i, *seq, stop)).id;
-    out.push_back(t);
-  }
+  auto step = [&](runtime::StageInput input, std::size_t position) {
+    const auto token = std::get<runtime::SampledToken>(stage->execute(std::move(input), position, *seq, stop));
+    if (logprobs) {
+      std::printf("TOP [");
+      for (std::size_t i = 0; i < token.top_logprobs.size(); ++i)
+        std::printf("%s[%llu,%.9g]", i ? "," : "", static_cast<unsigned long long>(token.top_logprobs[i].token_id),
+                    token.top_logprobs[i].logprob);
+      std::printf("]\n");
+    }
+    out.push_back(token.id);
+    return token.id;
+  };
+  auto t = step(runtime::TokenInput{prompt}, 0);
+  for (int i = 0; i < decodes; ++i) t = step(runtime::TokenInput{{t}}, prompt.size() + i);
   std::printf("TOKENS [");
   for (std::size_t i = 0; i < out.size(); ++i) std::printf("%s%llu", i ? "," : "", static_cast<unsigned long long>(out[i]));
   std::printf("]\n");
@@ -741,6 +813,127 @@ void gpu_scheduler_mixed_pass(const std::vector<std::string>& args) {
   CHECK(metrics.passes == 1 && metrics.mixed_passes == 1 && metrics.largest_pass_rows == 4);
 }
 
+// StageBackend::execute_profiled through the adapter (cpp/src/cuda/stage.cpp:234-239): the
+// same outputs as execute() bit for bit, with "embedding", one "layer" per owned layer, then
+// "to-wire" (a first stage of two) or "final_norm", "lm_head", "sampling" (a whole-model
+// stage). And the factory's diagnostics (backend_factory.hpp:31-39): the bytes the library
+// holds on the device follow stage creation and destruction, the peak resets to them, and
+// the device reports its identity and free memory.
+void gpu_adapter_profiled_and_diagnostics(const std::vector<std::string>& args) {
+  CHECK(args.size() == 1);
+  const fs::path dir = args[0];
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  backend::StageOptions options;
+  options.kv_cache_bytes = 16u << 20;
+  options.kv_block_tokens = 32;
+  options.max_sequences = 8;
+  options.max_pass_rows = 64;
+  backend::RocmBackendFactory factory(options);
+  const runtime::MemoryAmounts capacity{1ull << 40, 1ull << 40, 0, 0};
+  const auto before = factory.allocator_metrics();
+  CHECK(before && before->cached_bytes == 0);
+  std::atomic_bool go{false};
+  const std::vector<std::uint64_t> prompt{1, 4, 2, 8, 3};
+  {
+    auto first = factory.load(request_for(m, 0, 2), dir, capacity);
+    const auto held = factory.allocator_metrics();
+    CHECK(held->active_bytes >= before->active_bytes + first->weight_memory().device_bytes);
+    CHECK(held->peak_bytes >= held->active_bytes);
+    auto a = first->allocate_sequence(8), b = first->allocate_sequence(8);
+    const auto plain = std::get<runtime::BoundaryActivation>(first->execute(runtime::TokenInput{prompt}, 0, *a, go));
+    runtime::ExecutionTiming timing;
+    const auto timed = std::get<runtime::BoundaryActivation>(
+        first->execute_profiled(runtime::TokenInput{prompt}, 0, *b, go, timing));
+    CHECK(plain.tokens == timed.tokens && plain.payload == timed.payload);
+    CHECK(timing.components.size() == 3);
+    CHECK(timing.components[0].component == "embedding" && !timing.components[0].layer_index);
+    CHECK(timing.components[1].component == "layer" && timing.components[1].layer_index == 0);
+    CHECK(timing.components[2].component == "to-wire");
+    for (const auto& c : timing.components) CHECK(c.milliseconds >= 0.0);
+    {
+      auto whole = factory.load(request_for(m, 0, 1), dir, capacity);
+      CHECK(factory.allocator_metrics()->active_bytes > held->active_bytes);
+      auto c = whole->allocate_sequence(8), d = whole->allocate_sequence(8);
+      const auto t1 = std::get<runtime::SampledToken>(whole->execute(runtime::TokenInput{prompt}, 0, *c, go));
+      runtime::ExecutionTiming t;
+      const auto t2 = std::get<runtime::SampledToken>(whole->execute_profiled(runtime::TokenInput{prompt}, 0, *d, go, t));
+      CHECK(t1.id == t2.id);
+      std::vector<std::string> names;
+      for (const auto& x : t.components) names.push_back(x.component);
+      CHECK((names == std::vector<std::string>{"embedding", "layer", "layer", "final_norm", "lm_head", "sampling"}));
+      CHECK(t.components[1].layer_index == 0 && t.components[2].layer_index == 1);
+      // The sequences continue after a profiled pass.
+      static_cast<void>(whole->execute_profiled(runtime::TokenInput{{t2.id}}, prompt.size(), *d, go, t));
+      CHECK(t.components.size() == 6);
+    }
+    const auto after_whole = factory.allocator_metrics();
+    CHECK(after_whole->active_bytes == held->active_bytes && after_whole->peak_bytes > held->active_bytes);
+    CHECK(factory.profiling_reset_peak());
+    CHECK(factory.allocator_metrics()->peak_bytes == held->active_bytes);
+  }
+  CHECK(factory.allocator_metrics()->active_bytes == before->active_bytes);
+  const runtime::ProfilingDeviceInfo info = factory.profiling_device_info();
+  CHECK(info.identity.size() == 32 && !info.name.empty() && info.available_bytes && *info.available_bytes > 0);
+  CHECK(factory.boundary_transport_mode() == "pinned");
+  std::printf("DEVICE %s | %s | %s | driver %s\n", info.identity.c_str(), info.name.c_str(),
+              info.backend_version.c_str(), info.driver_version.c_str());
+}
+
+// In-pass cancellation through the adapter: another thread sets the request's flag while
+// the caller is inside execute(). A flag seen before the call throws without running
+// anything, and the sequence continues; a flag seen inside the pass (between layers or when
+// it completes) fails it with CANCELLED and the sequence is never resumed
+// (cpp/src/cpu/stage.cpp:109-111; cpp/src/cuda/stage.cpp:357,396,456,463-468); a pass that
+// completed first keeps its result. When the flag lands is up to timing: the attempts spread
+// it over the pass, and at least one must land inside.
+void gpu_adapter_cancellation(const std::vector<std::string>& args) {
+  CHECK(args.size() == 1);
+  const fs::path dir = args[0];
+  const model::ModelManifest m = model::manifest_from_checkpoint(dir);
+  backend::StageOptions options;
+  options.kv_cache_bytes = 64u << 20;
+  options.kv_block_tokens = 32;
+  options.max_sequences = 8;
+  options.max_pass_rows = 512;
+  backend::RocmBackendFactory factory(options);
+  auto stage = factory.load(request_for(m, 0, 1), dir, {1ull << 40, 1ull << 40, 0, 0});
+  const std::vector<std::uint64_t> prompt(400, 3);
+  std::atomic_bool no{false};
+  int inside = 0, before = 0, completed = 0;
+  for (int attempt = 0; attempt < 300 && inside < 3; ++attempt) {
+    auto seq = stage->allocate_sequence(prompt.size() + 2);
+    std::atomic_bool cancelled{false}, entered{false};
+    const long spin = (attempt * 7919L) % 400000L;
+    std::thread setter([&] {
+      while (!entered.load()) std::this_thread::yield();
+      for (volatile long i = 0; i < spin; i = i + 1) {
+      }
+      cancelled.store(true);
+    });
+    entered.store(true);
+    try {
+      static_cast<void>(stage->execute(runtime::TokenInput{prompt}, 0, *seq, cancelled));
+      setter.join();
+      ++completed;
+    } catch (const runtime::Error& e) {
+      setter.join();
+      CHECK(e.code() == runtime::ErrorCode::kCancelled);
+      ++inside;
+      EXPECT_ERROR(stage->execute(runtime::TokenInput{{1}}, prompt.size(), *seq, no), kInvalidRequest);
+      EXPECT_ERROR(stage->execute(runtime::TokenInput{prompt}, 0, *seq, no), kInvalidRequest);
+    } catch (const std::runtime_error&) {
+      setter.join();
+      ++before;
+      static_cast<void>(stage->execute(runtime::TokenInput{prompt}, 0, *seq, no));  // never started
+    }
+  }
+  std::printf("CANCELLATION inside %d, before %d, completed %d\n", inside, before, completed);
+  CHECK(inside >= 1);
+  // The stage still serves other sequences.
+  auto fresh = stage->allocate_sequence(8);
+  static_cast<void>(stage->execute(runtime::TokenInput{{1, 4, 2}}, 0, *fresh, no));
+}
+
 struct Case {
   const char* name;
   std::function<void(const std::vector<std::string>&)> run;
@@ -761,9 +954,14 @@ const std::vector<Case>& cases() {
       {"scheduler_without_mixed_passes", [](auto&) { scheduler_without_mixed_passes(true); }, false},
       {"scheduler_without_decode_batches", [](auto&) { scheduler_without_mixed_passes(false); }, false},
       {"scheduler_configuration", [](auto&) { scheduler_configuration(); }, false},
+      {"scheduler_classifies_first_tokens_as_prefills", [](auto&) { scheduler_classifies_first_tokens_as_prefills(); }, false},
+      {"scheduler_shutdown_with_queued_requests", [](auto&) { scheduler_shutdown(false); }, false},
+      {"scheduler_shutdown_during_a_pass", [](auto&) { scheduler_shutdown(true); }, false},
       {"gpu_checkpoint_greedy", gpu_checkpoint_greedy, true},
       {"gpu_decode_batch_contract", gpu_decode_batch_contract, true},
       {"gpu_scheduler_mixed_pass", gpu_scheduler_mixed_pass, true},
+      {"gpu_adapter_profiled_and_diagnostics", gpu_adapter_profiled_and_diagnostics, true},
+      {"gpu_adapter_cancellation", gpu_adapter_cancellation, true},
   };
   return all;
 }

@@ -198,6 +198,67 @@ def test_cancellation_before_and_during_a_pass():
     st.close()
 
 
+def test_cancel_poll_at_every_checkpoint():
+    """The cancel_poll callback is read where the flag is: once before the pass is enqueued,
+    before each of the stage's layers is enqueued, and once when the pass completes (1 + L + 1
+    polls). Cancelled at the first poll nothing ran and the sequence goes on; cancelled at
+    any later one the pass is discarded and its sequences are failed for good
+    (cpp/src/cpu/stage.cpp:109-111; cpp/src/cuda/stage.cpp:357,396,456,463-468)."""
+    _say("cancel poll checkpoints")
+    st = _stage()
+    layers = SHAPE.layers
+    calls = []
+    st.execute([capi.item(st.allocate(8), 3, 0)], token_ids=[1, 2, 3],
+               cancelled=lambda: calls.append(1) and False)
+    assert len(calls) == 1 + layers + 1
+    for at in range(1, layers + 3):
+        s = st.allocate(16)
+        seen = []
+
+        def poll():
+            seen.append(1)
+            return len(seen) == at
+
+        with pytest.raises(capi.StageError) as e:
+            st.execute([capi.item(s, 3, 0)], token_ids=[1, 2, 3], cancelled=poll)
+        assert e.value.status == capi.CANCELLED and len(seen) == at
+        assert st.length(s) == 0
+        if at == 1:
+            st.execute([capi.item(s, 3, 0)], token_ids=[1, 2, 3])  # never started: goes on
+            assert st.length(s) == 3
+        else:
+            with pytest.raises(capi.StageError) as e:
+                st.execute([capi.item(s, 3, 0)], token_ids=[1, 2, 3])
+            assert e.value.status == capi.INVALID_REQUEST
+        st.release(s)
+    st.close()
+
+
+def test_allocator_metrics_and_device_info():
+    """The factory diagnostics behind BackendFactory::allocator_metrics / profiling_reset_peak
+    / profiling_device_info (cpp/include/hllm/runtime/backend_factory.hpp:31-39): the bytes
+    held follow stage creation and destruction, no caching (cached 0), the peak resets to the
+    bytes held, and the device reports its identity and memory."""
+    _say("allocator metrics")
+    before = capi.allocator_metrics(0)
+    assert before["cached_bytes"] == 0 and before["peak_bytes"] >= before["active_bytes"]
+    st = _stage(kv_bytes=32 << 20)
+    held = capi.allocator_metrics(0)
+    assert held["active_bytes"] - before["active_bytes"] >= 16 << 20
+    st.close()
+    after = capi.allocator_metrics(0)
+    assert after["active_bytes"] == before["active_bytes"] and after["peak_bytes"] >= held["active_bytes"]
+    capi.reset_peak(0)
+    assert capi.allocator_metrics(0)["peak_bytes"] == after["active_bytes"]
+    info = capi.device_info(0)
+    _say("device", info)
+    assert len(info["identity"]) == 32 and info["name"] and info["architecture"].startswith("gfx950")
+    assert 0 < info["available_bytes"] <= info["total_bytes"] and info["compute_units"] > 0
+    with pytest.raises(capi.StageError) as e:
+        capi.device_info(1 << 20)
+    assert e.value.status == capi.INVALID_REQUEST
+
+
 @pytest.mark.parametrize("first,final", [(True, True), (True, False), (False, True)])
 def test_profiled_pass_equals_execute(first, final):
     """execute_profiled returns execute's outputs bit for bit, with one timed phase per

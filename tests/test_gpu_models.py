@@ -1,7 +1,8 @@
 """Whole-model greedy decoding on the GPU against the CPU oracle, through the C ABI, on
-the seeded synthetic Qwen3-0.6B (28 layers) and Qwen3-4B (36 layers), full vocabularies:
-two sequences prefilled in chunks inside shared ragged passes, then decoded together with
-device-fed tokens.
+the seeded synthetic Qwen3-0.6B (28 layers, full vocabulary, RMSNorm weights jittered): two
+sequences prefilled in small chunks inside shared ragged passes, then decoded together with
+device-fed tokens. (Qwen3-4B at full depth is checked over 65 greedy steps per sequence by
+tests/test_gpu_greedy_identity.py against a committed oracle fixture.)
 
 F32 execution must produce the oracle's greedy tokens exactly. F16 execution must produce
 the first LEADING tokens exactly, and may only depart after them at a step where the
@@ -16,12 +17,12 @@ from tests import models
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
-# F16 tokens that must equal the oracle's before any departure at a near tie (these seeded
-# runs measured every token equal: 11 of 11 for Qwen3-0.6B, 5 of 5 for Qwen3-4B).
+# F16 tokens that must equal the oracle's before any departure at a near tie (this seeded
+# run measured every token equal: 11 of 11).
 LEADING = 4
 # model -> (prompt lengths, prefill chunk, decode steps)
-PLANS = {"qwen3-0.6b": ({"a": 24, "b": 17}, 8, 10), "qwen3-4b": ({"a": 12, "b": 7}, 6, 4)}
-SHAPES = {"qwen3-0.6b": synthetic.QWEN3_0_6B, "qwen3-4b": synthetic.QWEN3_4B}
+PLANS = {"qwen3-0.6b": ({"a": 24, "b": 17}, 8, 10)}
+SHAPES = {"qwen3-0.6b": synthetic.QWEN3_0_6B}
 
 
 @pytest.fixture(scope="module", params=list(PLANS))

@@ -311,17 +311,19 @@ def _ref_layer(cfg, arrays):
 
 @needs_ref
 @pytest.mark.parametrize("qk_norm,rows_plan", [(1, [(0, 7), (7, 1), (8, 3)]),
-                                               (0, [(0, 1), (1, 5), (6, 1)])])
+                                               (0, [(0, 1), (1, 5), (6, 1)]),
+                                               # large enough for the threaded attention
+                                               (1, [(0, 260), (260, 1), (261, 120)])])
 def test_transformer_layer_equals_reference_bitwise(qk_norm, rows_plan):
     shape = synthetic.ModelShape("t", 1, 48, 80, 6, 2, 16, 97, theta=1e4, qk_norm=bool(qk_norm),
-                                 tied=True, dtype="f32", max_seq=64)
+                                 tied=True, dtype="f32", max_seq=512)
     w = models.synthetic_stage(shape, seed=5, norm_sigma=0.2)
     cfg = models.oracle_config(shape)
     arrays = w.layer(0)
     handle, keep = _ref_layer(cfg, arrays)
-    cache = REF.ref_cache_create(64, 2, 16)
+    cache = REF.ref_cache_create(512, 2, 16)
     kv = oracle._Kv()
-    oracle.lib().orc_kv_init(C.byref(kv), 64, 2, 16)
+    oracle.lib().orc_kv_init(C.byref(kv), 512, 2, 16)
     rng = np.random.default_rng(qk_norm)
     for first, rows in rows_plan:
         x = rng.standard_normal((rows, 48)).astype(np.float32)
