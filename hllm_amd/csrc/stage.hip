@@ -2,6 +2,7 @@
 // pool with a host-side block allocator, per-pass workspaces reserved up front, and the
 // pass pipeline (pack -> embed/decode -> layers -> head/argmax or boundary encode).
 #include <algorithm>
+#include <cctype>
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
@@ -1637,14 +1638,25 @@ hllm_rocm_device_info device_info(int32_t device) {
   hipDeviceProp_t p{};
   HIP_CHECK(hipGetDeviceProperties(&p, device));
   hllm_rocm_device_info out{};
+  // ROCm reports the UUID as 16 ASCII hex digits (the unique ID of the GPU); other bytes are
+  // written as hex.
+  bool ascii = true;
+  for (int i = 0; i < 16; ++i) ascii &= std::isxdigit(static_cast<unsigned char>(p.uuid.bytes[i])) != 0;
   static const char* hex = "0123456789abcdef";
   for (int i = 0; i < 16; ++i) {
     const unsigned char b = static_cast<unsigned char>(p.uuid.bytes[i]);
-    out.identity[2 * i] = hex[b >> 4];
-    out.identity[2 * i + 1] = hex[b & 15];
+    if (ascii) {
+      out.identity[i] = static_cast<char>(std::tolower(b));
+    } else {
+      out.identity[2 * i] = hex[b >> 4];
+      out.identity[2 * i + 1] = hex[b & 15];
+    }
   }
-  std::strncpy(out.name, p.name, sizeof(out.name) - 1);
   std::strncpy(out.architecture, p.gcnArchName, sizeof(out.architecture) - 1);
+  // The product name when the driver reports one, else the ISA name.
+  const std::string arch(p.gcnArchName);
+  const std::string name = p.name[0] ? std::string(p.name) : "AMD GPU " + arch.substr(0, arch.find(':'));
+  std::strncpy(out.name, name.c_str(), sizeof(out.name) - 1);
   HIP_CHECK(hipRuntimeGetVersion(&out.runtime_version));
   HIP_CHECK(hipDriverGetVersion(&out.driver_version));
   out.compute_units = (uint32_t)p.multiProcessorCount;

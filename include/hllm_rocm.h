@@ -142,8 +142,9 @@ typedef struct {
 } hllm_rocm_allocator_metrics;
 
 /* BackendFactory::profiling_device_info (cpp/include/hllm/runtime/profiling.hpp:8-15; the CUDA
- * worker's cpp/src/cuda/device.cpp:93-108): the device's identity (UUID, hex), product name,
- * ISA, HIP runtime and driver versions, compute units and free / total HBM. */
+ * worker's cpp/src/cuda/device.cpp:93-108): the device's identity (its UUID as hex digits:
+ * 16 as ROCm reports them, or 32 for binary UUIDs), product name (the ISA name when the driver
+ * reports none), ISA, HIP runtime and driver versions, compute units and free / total HBM. */
 typedef struct {
   char identity[40];
   char name[64];

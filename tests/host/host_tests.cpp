@@ -873,7 +873,8 @@ void gpu_adapter_profiled_and_diagnostics(const std::vector<std::string>& args) 
   }
   CHECK(factory.allocator_metrics()->active_bytes == before->active_bytes);
   const runtime::ProfilingDeviceInfo info = factory.profiling_device_info();
-  CHECK(info.identity.size() == 32 && !info.name.empty() && info.available_bytes && *info.available_bytes > 0);
+  CHECK((info.identity.size() == 16 || info.identity.size() == 32) && !info.name.empty() && info.available_bytes &&
+        *info.available_bytes > 0);
   CHECK(factory.boundary_transport_mode() == "pinned");
   std::printf("DEVICE %s | %s | %s | driver %s\n", info.identity.c_str(), info.name.c_str(),
               info.backend_version.c_str(), info.driver_version.c_str());

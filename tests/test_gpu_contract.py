@@ -252,7 +252,7 @@ def test_allocator_metrics_and_device_info():
     assert capi.allocator_metrics(0)["peak_bytes"] == after["active_bytes"]
     info = capi.device_info(0)
     _say("device", info)
-    assert len(info["identity"]) == 32 and info["name"] and info["architecture"].startswith("gfx950")
+    assert len(info["identity"]) in (16, 32) and info["name"] and info["architecture"].startswith("gfx950")
     assert 0 < info["available_bytes"] <= info["total_bytes"] and info["compute_units"] > 0
     with pytest.raises(capi.StageError) as e:
         capi.device_info(1 << 20)

@@ -53,14 +53,19 @@ def test_host_cases_under_sanitizers(kind):
         assert r.returncode == 0 and f"PASS {case}" in r.stdout, (kind, case, r.stdout + r.stderr)
 
 
-def _write_tiny_checkpoint(path):
+def _write_tiny_checkpoint(path, max_positions=None):
+    """The reference's tiny Qwen3 fixture as a checkpoint (`max_positions` overrides its
+    context of 32 positions, for longer passes)."""
     from safetensors.numpy import save_file
     fx = models.tiny_reference()
     w = models.tiny_reference_stage()
     save_file({k: np.ascontiguousarray(v, np.float32) for k, v in w.tensors.items()},
               str(path / "model.safetensors"))
+    cfg = dict(fx["config"])
+    if max_positions:
+        cfg["max_position_embeddings"] = max_positions
     with open(path / "config.json", "w") as f:
-        json.dump(fx["config"], f)
+        json.dump(cfg, f)
     return w
 
 
@@ -162,7 +167,7 @@ def test_adapter_execute_profiled_and_factory_diagnostics(tmp_path):
 
 @pytest.mark.gpu
 def test_adapter_cancels_inside_a_pass_and_fails_the_sequence(tmp_path):
-    _write_tiny_checkpoint(tmp_path)
+    _write_tiny_checkpoint(tmp_path, max_positions=1024)
     print(_run("gpu_adapter_cancellation", tmp_path, timeout=120))
 
 
