@@ -93,6 +93,7 @@ class Engine:
                                  np.zeros(concurrency + chunk, np.uint64), capi.Pass()))
         self.flip = 0
         self.current = None  # the submitted pass: (sampled, rows, decode rows, finished)
+        self.work = None     # StepWork accumulating the submitted passes' algorithmic work
 
     def _plan(self):
         """Admits arrivals and builds the next pass; None for an idle step."""
@@ -143,6 +144,8 @@ class Engine:
         if plan is None:  # nothing has arrived yet: an idle step launches nothing
             return (0, 0, 0, [], False, 0)
         p, rows, decode, prefill = plan
+        if self.work is not None:
+            self.work.add(decode, prefill)
         capi.check(self.stage.lib.hllm_rocm_stage_submit(self.stage.handle, C.byref(p)))
         sampled = len(decode)
         finished = []
@@ -232,6 +235,44 @@ class Engine:
 
 # ------------------------------------------------------------------ measurements
 
+class StepWork:
+    """Algorithmic HBM bytes and FLOPs of submitted workload passes, and the time each pass
+    needs at the roofline (the longer of its bytes at 8 TB/s and its FLOPs at 2.5 PFLOP/s).
+    A pass reads every layer weight once (and the LM head when it samples), reads each
+    item's cached keys and values once and writes its new ones; FLOPs are 2 per weight and
+    row (the head only for sampled rows) plus attention's 4 * heads * head_dim per (query,
+    attended key) pair per layer."""
+
+    def __init__(self, shape):
+        self.shape = shape
+        self.layer_params = shape.layers * (shape.layer_weight_bytes() // 2)
+        self.head_params = shape.vocab * shape.hidden
+        self.kv_tok = shape.kv_bytes_per_token()
+        self.passes, self.bytes, self.flops, self.roof_s, self.hbm_passes = 0, 0.0, 0.0, 0.0, 0
+
+    def add(self, decode, prefill):
+        s = self.shape
+        rows = len(decode) + sum(t for _, t in prefill)
+        sampled = len(decode) + sum(1 for r, t in prefill if r.fed + t == len(r.prompt))
+        kv_read = sum(r.length for r in decode) + sum(r.length for r, _ in prefill)
+        pairs = sum(r.length + 1 for r in decode) + sum(t * r.length + t * (t + 1) // 2 for r, t in prefill)
+        nbytes = 2 * (self.layer_params + (self.head_params if sampled else 0)) + (kv_read + rows) * self.kv_tok
+        flops = 2.0 * rows * self.layer_params + 2.0 * sampled * self.head_params + \
+            4.0 * s.heads * s.head_dim * s.layers * pairs
+        t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_F16_PEAK_TFLOPS * 1e12)
+        self.passes += 1
+        self.bytes += nbytes
+        self.flops += flops
+        self.roof_s += max(t_hbm, t_mfma)
+        self.hbm_passes += t_hbm >= t_mfma
+
+    def summary(self, elapsed):
+        return {"frac": self.roof_s / elapsed, "roofline_ms_per_step": 1e3 * self.roof_s / self.passes,
+                "bytes_per_step": self.bytes / self.passes, "flops_per_step": self.flops / self.passes,
+                "hbm_bound_steps": self.hbm_passes, "steps": self.passes,
+                "hbm_gb_s": self.bytes / elapsed / 1e9, "tflops": self.flops / elapsed / 1e12}
+
+
 def decode_bench(stage, shape, rng, rows, steps):
     """Pure decode passes: `rows` sequences prefilled to workload-distributed lengths."""
     lengths = [int(np.clip(round(math.exp(math.log(256.0) + rng.standard_normal())), 16, 2048))
@@ -311,6 +352,62 @@ def prefill_bench(stage, shape, rng, past, reps):
             "tflops": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
 
 
+def stage_share_bench(rng, steps, rows=128, first_layer=18):
+    """One pipeline stage's share at its real shape: Qwen3-4B layers 18-35 plus the final
+    norm and LM head behind an F16 boundary, 128 decode rows whose KV caches hold
+    log-uniform lengths in [1, 8192] (prefilled by untimed passes of N(0, 1) boundary rows),
+    greedy. Each timed step feeds 128 fresh N(0, 1) boundary rows from host memory (the
+    boundary crosses PCIe, as it does between pipeline stages) and returns the tokens."""
+    full = synthetic.QWEN3_4B
+    layers = full.layers - first_layer
+    lengths = np.exp(rng.uniform(0.0, math.log(8192.0), rows)).astype(np.int64)
+    lengths = np.clip(lengths, 1, 8192)
+    cfg = model.stage_config(full, first_layer, full.layers, False, True, execution="f16",
+                             kv_cache_bytes=int((lengths.sum() + rows * (steps + 40)) * 73728 * 1.1) + (1 << 30),
+                             max_sequences=rows + 8, max_pass_rows=2048, max_seq=8192 + steps + 64)
+    stage = capi.Stage(cfg)
+    model.synthesize(stage, full, seed=0, norm_sigma=0.0)
+    seqs = [stage.allocate(int(n) + steps + 8) for n in lengths]
+    pieces = []
+    for s_, n in zip(seqs, lengths):
+        for pos in range(0, int(n), 2048):
+            pieces.append((s_, pos, min(2048, int(n) - pos)))
+    batch, rows_in = [], 0
+    for piece in pieces + [None]:
+        if piece is None or rows_in + piece[2] > 2048:
+            if batch:
+                b = np.asarray(rng.standard_normal((rows_in, full.hidden)), np.float16).view(np.uint16)
+                stage.execute([capi.item(q, t, pos, sample=False) for q, pos, t in batch], boundary=b)
+            batch, rows_in = [], 0
+        if piece is not None:
+            batch.append(piece)
+            rows_in += piece[2]
+    ctx = lengths.copy()
+    times = []
+    for i in range(steps + 2):
+        items = [capi.item(q, 1, int(c)) for q, c in zip(seqs, ctx)]
+        b = np.asarray(rng.standard_normal((rows, full.hidden)), np.float16).view(np.uint16)
+        t0 = time.perf_counter()
+        stage.execute(items, boundary=b)
+        if i >= 2:  # two untimed passes first
+            times.append(time.perf_counter() - t0)
+        ctx += 1
+    for q in seqs:
+        stage.release(q)
+    stage.close()
+    kv_tok = full.kv_bytes_per_token(layers)
+    weights = layers * full.layer_weight_bytes() + full.vocab * full.hidden * 2
+    mean_ctx = float(lengths.mean()) + 2 + (steps - 1) / 2
+    bytes_per_step = weights + rows * (mean_ctx + 1) * kv_tok
+    t = float(np.mean(times))
+    return {"workload": f"Qwen3-4B layers {first_layer}-{full.layers - 1} + final norm and LM head, F16 "
+                        f"boundary input, {rows} decode rows, KV lengths log-uniform in [1, 8192]",
+            "rows": rows, "steps": steps, "mean_context": mean_ctx, "ms_per_step": 1e3 * t,
+            "tok_s": rows / t, "bytes_per_step": bytes_per_step, "hbm_gb_s": bytes_per_step / t / 1e9,
+            "hbm_frac": bytes_per_step / t / 1e9 / HBM_PEAK_GBS,
+            "roofline_ms_per_step": 1e3 * bytes_per_step / (HBM_PEAK_GBS * 1e9)}
+
+
 def cpu_baseline(shape, mean_context):
     """The reference CPU worker's own arithmetic (oracle/_ref, compiled from its sources),
     one thread: one decode step of one Qwen3-4B layer at the workload's mean context, and
@@ -387,7 +484,18 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with three plain 1 GiB device copies (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--region-markers", action="store_true",
+                    help="a 1 MiB device copy right before and right after the timed region, so "
+                         "that counter runs can select the region's dispatches")
+    ap.add_argument("--timed-only", action="store_true",
+                    help="stop after the timed region (counter runs)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarize two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "--timed-only --region-markers --copy-calibration into profiles/traffic.json")
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU: the stage worker runs the whole model (or one "
                  "pipeline stage's share) on a single MI355X; multi-GPU runs are not part of "
@@ -424,6 +532,9 @@ def main():
     engine.drain()
 
     # The timed region starts with no pass in flight and ends when its K-th pass completes.
+    if args.region_markers:
+        region_marker()
+    engine.work = StepWork(shape)
     step_ms, tokens, rows_total, decode_rows, active_total = [], 0, 0, 0, 0
     t_start = time.perf_counter()
     for i in range(args.steps):
@@ -435,9 +546,24 @@ def main():
         decode_rows += d
         active_total += a
     elapsed = time.perf_counter() - t_start
+    step_roofline = engine.work.summary(elapsed)
+    engine.work = None
+    if args.region_markers:
+        region_marker()
     mean_active = active_total / args.steps
     log(f"timed {args.steps} steps in {elapsed:.3f}s: {tokens} tokens, {rows_total} rows "
         f"({decode_rows} decode rows), {mean_active:.1f} requests per pass on average")
+    log("workload step roofline:", json.dumps(step_roofline))
+    if args.timed_only:
+        engine.release_all()
+        stage.close()
+        print(json.dumps({"metric": METRIC, "value": tokens / elapsed, "unit": "tok/s",
+                          "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": 1e3 * elapsed / args.steps, "step_roofline": step_roofline}),
+              flush=True)
+        if args.copy_calibration:
+            copy_calibration()
+        return
     # The dominant kernel: most HIP-event time over steps that continue the same steady
     # workload (events perturb the host's launch rate, so the throughput region above runs
     # without them).
@@ -510,6 +636,7 @@ def main():
         "latency_ms": {"p50": float(np.percentile(step_ms, 50)),
                        "p99": float(np.percentile(step_ms, 99))},
         "roofline": roof,
+        "step_roofline": step_roofline,
     }
     if not at_target:
         result["error"] = (f"the timed passes held {mean_active:.1f} requests on average, below the "
@@ -521,14 +648,107 @@ def main():
         result["decode"]["hbm_frac_of_read_ceiling"] = result["decode"]["hbm_gb_s"] / peak
         log("decode:", json.dumps({k: v for k, v in result["decode"].items() if k != "kernels"}))
         result["prefill"] = [prefill_bench(stage, shape, rng, past, 3) for past in (0, 1536)]
+        ceiling = {str(k): capi.measure_mfma_rate(k) for k in (16, 32)}
+        best = max(ceiling.values())
+        for entry in result["prefill"]:
+            entry["mfma_ceiling_tflops"] = best
+            entry["mfma_frac_of_ceiling"] = entry["tflops"] / best
+        result["mfma_ceiling_tflops"] = {"v_mfma_f32_16x16x32_f16": ceiling["16"],
+                                         "v_mfma_f32_32x32x16_f16": ceiling["32"],
+                                         "spec_dense_f16": MFMA_F16_PEAK_TFLOPS}
         log("prefill:", json.dumps(result["prefill"]))
+        log("MFMA ceiling:", json.dumps(result["mfma_ceiling_tflops"]))
     stage.close()
+    if not args.skip_extras:
+        result["stage_share"] = stage_share_bench(np.random.default_rng(args.seed + 3), args.decode_steps)
+        log("stage share:", json.dumps(result["stage_share"]))
     if not args.no_cpu_baseline:
         mean_ctx = result.get("decode", {}).get("mean_context", 483.0)
         result["cpu_baseline"] = cpu_baseline(synthetic.QWEN3_4B, mean_ctx)
     print(json.dumps(result), flush=True)
     if args.copy_calibration:
         copy_calibration()
+
+
+def region_marker():
+    """A 1 MiB device-to-device copy (the runtime's blit kernel) that counter runs find
+    before and after the timed region."""
+    hip = C.CDLL("libamdhip64.so")
+    n = 1 << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    for ptr in (src, dst):
+        if hip.hipMalloc(C.byref(ptr), C.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    try:
+        if hip.hipMemcpy(dst, src, C.c_size_t(n), 3) != 0 or hip.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipMemcpy failed")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """Per-kernel HBM bytes per launch over the timed region only: the dispatches between the
+    two 1 MiB marker copies of a --timed-only --region-markers --copy-calibration run, FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch) each scaled by what the counter reads for the 1 GiB
+    copies after the region. Kernels launched with several grid sizes (the decode GEMM runs
+    the projections and the LM head) are also kept per grid size."""
+    import csv
+
+    def load(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"].startswith(counter)]
+        per = collections.OrderedDict()
+        for r in rows:
+            d = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"], "grid": int(r["Grid_Size"]),
+                                                       "value": 0.0})
+            d["value"] += float(r["Counter_Value"])
+        return per
+
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        per = load(path, counter)
+        ids = sorted(per)
+        copies = [i for i in ids if "copyBuffer" in per[i]["name"]]
+        markers = [i for i in copies if per[i]["grid"] < (1 << 21)]
+        big = [i for i in copies if per[i]["grid"] >= (1 << 21)]
+        if len(markers) < 2 or not big:
+            raise SystemExit(f"{path}: expected two marker copies and the 1 GiB calibration copies")
+        lo, hi = markers[0], markers[-1]
+        scale_key = "fetch" if counter == "FETCH_SIZE" else "write"
+        cal = sum(per[i]["value"] for i in big) / len(big)
+        scale = (1 << 20) / cal  # KiB per GiB copied -> bytes factor: a GiB copy reads and writes 1 GiB
+        out[scale_key] = {"kib_per_gib_copy": cal, "scale": scale, "kernels": collections.defaultdict(list)}
+        for i in ids:
+            if lo < i < hi and "copyBuffer" not in per[i]["name"]:
+                name = per[i]["name"].split("(")[0].replace("hllm_rocm::(anonymous namespace)::", "")
+                out[scale_key]["kernels"][name].append((per[i]["grid"], per[i]["value"]))
+    kernels = {}
+    for name, f in out["fetch"]["kernels"].items():
+        w = out["write"]["kernels"].get(name, [])
+        if len(w) != len(f):
+            continue
+        entry = {"dispatches": len(f), "fetch_kib_per_dispatch": sum(v for _, v in f) / len(f),
+                 "write_kib_per_dispatch": sum(v for _, v in w) / len(w)}
+        entry["bytes_per_launch"] = 1024 * (entry["fetch_kib_per_dispatch"] * out["fetch"]["scale"] +
+                                            entry["write_kib_per_dispatch"] * out["write"]["scale"])
+        grids = sorted({g for g, _ in f})
+        if len(grids) > 1:
+            entry["by_grid"] = {}
+            for g in grids:
+                fv = [v for gg, v in f if gg == g]
+                wv = [v for gg, v in w if gg == g]
+                entry["by_grid"][str(g)] = {"dispatches": len(fv), "bytes_per_launch": 1024 * (
+                    sum(fv) / len(fv) * out["fetch"]["scale"] + sum(wv) / len(wv) * out["write"]["scale"])}
+        kernels[name] = entry
+    doc = {"region": "the timed region's dispatches only (between the marker copies)",
+           "copy_calibration": {"fetch_kib_per_gib_copy": out["fetch"]["kib_per_gib_copy"],
+                                "write_kib_per_gib_copy": out["write"]["kib_per_gib_copy"],
+                                "fetch_scale": out["fetch"]["scale"], "write_scale": out["write"]["scale"]},
+           "kernels": kernels}
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    with open(path, "w") as f:
+        json.dump(doc, f, indent=1)
+    print(json.dumps(doc, indent=1))
 
 
 def measured_traffic(kernel):

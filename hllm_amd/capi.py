@@ -32,7 +32,7 @@ EXPORTS = ("hllm_rocm_last_error", "hllm_rocm_abi_version", "hllm_rocm_stage_cre
            "hllm_rocm_stage_set_graphs", "hllm_rocm_stage_graph_stats", "hllm_rocm_set_gemm_config",
            "hllm_rocm_measure_read_bandwidth", "hllm_rocm_stage_execute_profiled",
            "hllm_rocm_sample_logits_noalloc", "hllm_rocm_device_allocator_metrics",
-           "hllm_rocm_device_reset_peak", "hllm_rocm_device_query")
+           "hllm_rocm_device_reset_peak", "hllm_rocm_device_query", "hllm_rocm_measure_mfma_rate")
 NOALLOC_MAX_VOCABULARY = 262144
 
 
@@ -146,6 +146,7 @@ def library() -> C.CDLL:
     L.hllm_rocm_stage_graph_stats.argtypes = [vp, C.POINTER(u64), C.POINTER(u64)]
     L.hllm_rocm_set_gemm_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
     L.hllm_rocm_measure_read_bandwidth.argtypes = [C.c_int32, u64, C.POINTER(C.c_double)]
+    L.hllm_rocm_measure_mfma_rate.argtypes = [C.c_int32, u32, C.POINTER(C.c_double)]
     L.hllm_rocm_sample_logits.argtypes = [C.c_int32, C.POINTER(C.c_float), u64, u64, C.POINTER(Item),
                                           C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64),
                                           C.POINTER(C.c_double)]
@@ -448,6 +449,14 @@ def measure_read_bandwidth(nbytes: int = 4 << 30, device: int = 0) -> float:
     """Measured HBM read ceiling of the device in GB/s (best of five streaming reads)."""
     out = C.c_double(0.0)
     check(library().hllm_rocm_measure_read_bandwidth(device, nbytes, C.byref(out)))
+    return out.value
+
+
+def measure_mfma_rate(shape: int = 16, device: int = 0) -> float:
+    """Measured F16 MFMA rate of the device in TFLOP/s, no memory traffic (shape 16:
+    v_mfma_f32_16x16x32_f16, 32: v_mfma_f32_32x32x16_f16)."""
+    out = C.c_double(0.0)
+    check(library().hllm_rocm_measure_mfma_rate(device, shape, C.byref(out)))
     return out.value
 
 

@@ -68,6 +68,7 @@ inline const char* kernel_name(const char* base) {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ F-layout
 //

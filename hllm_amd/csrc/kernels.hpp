@@ -129,6 +129,8 @@ __host__ __device__ inline uint64_t kv_value_index(const KvView& kv, int layer, 
 
 // Streaming read of `bytes` (a multiple of 16) from p: a measured HBM read ceiling.
 void launch_read_probe(hipStream_t stream, const void* p, size_t bytes, float* out);
+// MFMA issue-rate probe (shape 16: 16x16x32 F16, 32: 32x32x16 F16); returns the FLOPs launched.
+double launch_mfma_probe(hipStream_t stream, int shape, int blocks, int iters, float* out);
 void launch_pack(hipStream_t stream, const ItemMeta* items, int n_items, const int32_t* host_tokens,
                  const int32_t* last_token, const int32_t* block_table, int table_width,
                  int block_tokens, PackOut out);

@@ -673,9 +673,59 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const floatx4* p, size_
   if (acc[0] == -1234.5f) out[0] = acc[1];
 }
 
+// ------------------------------------------------------------------ MFMA rate probe
+
+// Eight independent accumulation chains per wave of one F16 MFMA shape (16 = 16x16x32,
+// 32 = 32x32x16), operands from registers: the issue rate of the matrix cores with no
+// memory traffic. The sums are stored only if they equal a value they never take.
+template <int SHAPE>
+__global__ void __launch_bounds__(256) mfma_probe_kernel(int iters, float* out) {
+  half8 a, b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    a[j] = (_Float16)((threadIdx.x & 7) * 0.125f + j);
+    b[j] = (_Float16)((threadIdx.x >> 3) * 0.0625f - j);
+  }
+  float total = 0.f;
+  if constexpr (SHAPE == 16) {
+    floatx4 acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[k], 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) total += acc[k][0] + acc[k][3];
+  } else {
+    floatx16 acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[k], 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) total += acc[k][0] + acc[k][15];
+  }
+  if (total == -1234.5f) out[0] = total;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
+
+double launch_mfma_probe(hipStream_t stream, int shape, int blocks, int iters, float* out) {
+  if (shape == 16) {
+    observed("mfma_probe_kernel<16>", [&] { mfma_probe_kernel<16><<<blocks, 256, 0, stream>>>(iters, out); });
+  } else {
+    observed("mfma_probe_kernel<32>", [&] { mfma_probe_kernel<32><<<blocks, 256, 0, stream>>>(iters, out); });
+  }
+  // FLOPs: blocks x 4 waves x iters x 8 chains x (16 x 16 x 32 or 32 x 32 x 16) x 2.
+  return (double)blocks * 4 * iters * 8 * (shape == 16 ? 16.0 * 16 * 32 : 32.0 * 32 * 16) * 2.0;
+}
 
 void launch_read_probe(hipStream_t stream, const void* p, size_t bytes, float* out) {
   observed("read_probe_kernel", [&] {

@@ -1709,6 +1709,45 @@ double measure_read_bandwidth(int32_t device, uint64_t bytes) {
   return best;
 }
 
+// Best of five timed launches of the MFMA probe over every CU (eight workgroups of four
+// waves per CU, eight independent accumulation chains per wave), in TFLOP/s.
+double measure_mfma_rate(int32_t device, uint32_t shape) {
+  if (shape != 16 && shape != 32) fail(HLLM_INVALID_REQUEST, "MFMA probe shape must be 16 or 32");
+  HIP_CHECK(hipSetDevice(device));
+  int cus = 256;
+  HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  DeviceMemory out;
+  out.allocate(sizeof(float), "MFMA probe");
+  hipStream_t s = nullptr;
+  HIP_CHECK(hipStreamCreate(&s));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  double best = 0.0;
+  try {
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    const int blocks = 8 * cus, iters = 2048;
+    launch_mfma_probe(s, (int)shape, blocks, iters / 8, out.as<float>());
+    for (int i = 0; i < 5; ++i) {
+      HIP_CHECK(hipEventRecord(e0, s));
+      const double flops = launch_mfma_probe(s, (int)shape, blocks, iters, out.as<float>());
+      HIP_CHECK(hipEventRecord(e1, s));
+      HIP_CHECK(hipEventSynchronize(e1));
+      float ms = 0.f;
+      HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+      best = std::max(best, flops / (ms * 1e-3) / 1e12);
+    }
+  } catch (...) {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(s);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipStreamDestroy(s);
+  return best;
+}
+
 void sample_logits(int32_t device, const float* logits, uint64_t rows, uint64_t V, const hllm_rocm_item* options,
                    uint64_t* tokens, double* logprobs, uint64_t* top_ids, double* top_logprobs) {
   if (!logits || !options || !tokens || rows == 0 || V == 0) fail(HLLM_INVALID_REQUEST, "invalid sampling request");
@@ -1981,6 +2020,13 @@ hllm_status hllm_rocm_device_query(int32_t device, hllm_rocm_device_info* out) {
   return guarded([&] {
     if (!out) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null output");
     *out = hllm_rocm::device_info(device);
+  });
+}
+
+hllm_status hllm_rocm_measure_mfma_rate(int32_t device, uint32_t shape, double* tflops) {
+  return guarded([&] {
+    if (!tflops) hllm_rocm::fail(HLLM_INVALID_REQUEST, "null output");
+    *tflops = hllm_rocm::measure_mfma_rate(device, shape);
   });
 }
 

@@ -282,6 +282,14 @@ hllm_status hllm_rocm_device_query(int32_t device, hllm_rocm_device_info* out);
  * counterpart in the reference. */
 hllm_status hllm_rocm_measure_read_bandwidth(int32_t device, uint64_t bytes, double* gb_s);
 
+/* Diagnostics: the F16 matrix-core rate of `device` in TFLOP/s with no memory traffic, for
+ * v_mfma_f32_16x16x32_f16 (shape 16) or v_mfma_f32_32x32x16_f16 (shape 32): best of five
+ * launches of eight workgroups of four waves per CU, each wave running eight independent
+ * accumulation chains from registers. The measured ceiling the prefill GEMMs' MFMA fractions
+ * are read against beside the 2.5 PFLOP/s dense F16 specification; no counterpart in the
+ * reference. */
+hllm_status hllm_rocm_measure_mfma_rate(int32_t device, uint32_t shape, double* tflops);
+
 /* Tuning and test hook, process-wide: every later projection GEMM uses configuration
  * `config` of the kernel table (0 .. 18; 17: the decode kernel for every F16 projection of at
  * most 64 rows whose K splits are summed by the consumer or that applies SwiGLU) instead of the

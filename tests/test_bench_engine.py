@@ -102,3 +102,30 @@ def test_prestart_reaches_the_stated_concurrency(monkeypatch):
     assert min(active) >= 15 and np.mean(active) >= 0.95 * 16
     engine.release_all()
     assert not any(stage.live.values())
+
+
+def test_step_work_closed_form():
+    """The workload step roofline's algorithmic work of one pass holding a decode row at
+    context 100 and a 512-token prefill chunk that completes its prompt: every layer weight
+    and the LM head read once, 100 cached positions read and 513 written, FLOPs 2 per weight
+    and row (the head for the two sampled rows) plus attention's 4 * heads * head_dim per
+    (query, key) pair per layer."""
+    from hllm_amd import synthetic
+    shape = synthetic.QWEN3_4B
+
+    class Req:
+        def __init__(self, length, fed, prompt):
+            self.length, self.fed, self.prompt = length, fed, [0] * prompt
+
+    w = bench.StepWork(shape)
+    w.add([Req(100, 10, 10)], [(Req(0, 0, 512), 512)])
+    params = 36 * (4096 * 2560 + 2 * 1024 * 2560 + 2560 * 4096 + 3 * 9728 * 2560 + 2 * 2560 + 2 * 128)
+    head = 151936 * 2560
+    kv_tok = 36 * 8 * 128 * 2 * 2
+    assert w.bytes == 2 * (params + head) + (100 + 513) * kv_tok
+    pairs = 101 + 512 * 513 // 2
+    assert w.flops == 2.0 * 513 * params + 2.0 * 2 * head + 4.0 * 32 * 128 * 36 * pairs
+    t = max(w.bytes / 8e12, w.flops / 2.5e15)
+    assert abs(w.roof_s - t) < 1e-15 and w.hbm_passes == 0
+    s = w.summary(2 * t)
+    assert abs(s["frac"] - 0.5) < 1e-12 and s["steps"] == 1
