@@ -687,6 +687,22 @@ def region_marker():
         hip.hipFree(dst)
 
 
+def kernel_key(profiler_name):
+    """A kernel as the stage's profiling records name it ("gemm_decode_kernel<4, 8, 1, 4, 4, 0>")
+    from its name in a rocprofv3 CSV ("void hllm_rocm::(anonymous namespace)::gemm_decode_kernel<4,
+    8, 1, 4, 4, false>(hllm_rocm::GemmArgs, int, int)")."""
+    name = profiler_name.replace("void ", "", 1).replace("hllm_rocm::(anonymous namespace)::", "")
+    name = name.replace("hllm_rocm::", "")
+    depth, cut = 0, len(name)
+    for j, ch in enumerate(name):
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            cut = j
+            break
+    return name[:cut].replace("true", "1").replace("false", "0").strip()
+
+
 def traffic_summary(fetch_csv, write_csv):
     """Per-kernel HBM bytes per launch over the timed region only: the dispatches between the
     two 1 MiB marker copies of a --timed-only --region-markers --copy-calibration run, FETCH_SIZE
@@ -708,10 +724,13 @@ def traffic_summary(fetch_csv, write_csv):
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         per = load(path, counter)
         ids = sorted(per)
+        # The runtime's copy kernel also runs the stage's small copies: the 1 GiB calibration
+        # copies are the largest grids, the two 1 MiB markers the next largest.
         copies = [i for i in ids if "copyBuffer" in per[i]["name"]]
-        markers = [i for i in copies if per[i]["grid"] < (1 << 21)]
-        big = [i for i in copies if per[i]["grid"] >= (1 << 21)]
-        if len(markers) < 2 or not big:
+        grids = sorted({per[i]["grid"] for i in copies}, reverse=True)
+        big = [i for i in copies if per[i]["grid"] == grids[0]] if grids else []
+        markers = [i for i in copies if len(grids) > 1 and per[i]["grid"] == grids[1]]
+        if len(markers) != 2 or len(big) < 1:
             raise SystemExit(f"{path}: expected two marker copies and the 1 GiB calibration copies")
         lo, hi = markers[0], markers[-1]
         scale_key = "fetch" if counter == "FETCH_SIZE" else "write"
@@ -720,8 +739,7 @@ def traffic_summary(fetch_csv, write_csv):
         out[scale_key] = {"kib_per_gib_copy": cal, "scale": scale, "kernels": collections.defaultdict(list)}
         for i in ids:
             if lo < i < hi and "copyBuffer" not in per[i]["name"]:
-                name = per[i]["name"].split("(")[0].replace("hllm_rocm::(anonymous namespace)::", "")
-                out[scale_key]["kernels"][name].append((per[i]["grid"], per[i]["value"]))
+                out[scale_key]["kernels"][kernel_key(per[i]["name"])].append((per[i]["grid"], per[i]["value"]))
     kernels = {}
     for name, f in out["fetch"]["kernels"].items():
         w = out["write"]["kernels"].get(name, [])
