@@ -55,6 +55,9 @@ __device__ inline float* partial_at(const AttentionArgs& a, int row, int qh, int
   return a.partial + (((size_t)row * a.q_heads + qh) * a.max_splits + split) * (a.head_dim + 2);
 }
 
+template <int E, bool kCoherent>
+__device__ inline void merge_splits(const AttentionArgs& a, int r, int qh, int splits, int lane);
+
 // ---------------------------------------------------------------- MFMA flash attention
 
 // LDS of the MFMA kernel: the split-key merge uses [128 + 4 * D * 16] floats; fused decode
@@ -516,6 +519,10 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     }
   }
 
+  // Decode-like blocks with split keys merge them here: the split workgroup that arrives
+  // last (a device-scope count per block and KV head) merges every split in split order,
+  // with the combine kernel's arithmetic. Workgroup-uniform.
+  const bool fold = split_keys && w.splits > 1 && a.fold;
   float m_fin = m, l_fin = l;
   if (split_keys) {
     // Merge the four waves' partial softmax states (vectors 0..15) through LDS. A lane's
@@ -533,31 +540,68 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
       for (int df = 0; df < DF; ++df) sm_o[(wave * DF + df) * 64 + lane] = o[df];
     }
     __syncthreads();
-    if (wave != 0) return;
-    float mm = -INFINITY;
+    if (wave != 0 && !fold) return;
+    if (wave == 0) {
+      float mm = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) mm = fmaxf(mm, sm_m[ww * 16 + col]);
-    float weights[4];
-    l_fin = 0.0f;
+      for (int ww = 0; ww < 4; ++ww) mm = fmaxf(mm, sm_m[ww * 16 + col]);
+      float weights[4];
+      l_fin = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      weights[ww] = exp2_fast(sm_m[ww * 16 + col] - (mm == -INFINITY ? 0.0f : mm));
-      l_fin += sm_l[ww * 16 + col] * weights[ww];
-    }
-    m_fin = mm;
+      for (int ww = 0; ww < 4; ++ww) {
+        weights[ww] = exp2_fast(sm_m[ww * 16 + col] - (mm == -INFINITY ? 0.0f : mm));
+        l_fin += sm_l[ww * 16 + col] * weights[ww];
+      }
+      m_fin = mm;
 #pragma unroll
-    for (int df = 0; df < DF; ++df) {
-      floatx4 others[3];
+      for (int df = 0; df < DF; ++df) {
+        floatx4 others[3];
 #pragma unroll
-      for (int ww = 1; ww < 4; ++ww) others[ww - 1] = sm_o[(ww * DF + df) * 64 + lane];
+        for (int ww = 1; ww < 4; ++ww) others[ww - 1] = sm_o[(ww * DF + df) * 64 + lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float s = 0.0f + o[df][i] * weights[0];
+        for (int i = 0; i < 4; ++i) {
+          float s = 0.0f + o[df][i] * weights[0];
 #pragma unroll
-        for (int ww = 1; ww < 4; ++ww) s += others[ww - 1][i] * weights[ww];
-        o[df][i] = s;
+          for (int ww = 1; ww < 4; ++ww) s += others[ww - 1][i] * weights[ww];
+          o[df][i] = s;
+        }
       }
     }
+  }
+  if (fold) {
+    // Wave 0 publishes this split's partial with device-scope stores, waits for them to
+    // complete and counts the arrival; the count's last arrival resets it for the next
+    // launch and the four waves merge the block's vectors. No cache-wide fence is needed:
+    // every access to the partials and the count is device-coherent on its own.
+    int32_t* arrivals = a.split_arrivals + (size_t)w.row0 * a.kv_heads + kvh;
+    int* arrived = reinterpret_cast<int*>(smem);  // wave 0 has finished reading the merge area
+    if (wave == 0) {
+      if (v_ok) {
+        float* out = partial_at(a, w.row0 + vr, kvh * G + vg, w.split);
+#pragma unroll
+        for (int df = 0; df < DF; ++df)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            __hip_atomic_store(out + 16 * df + 4 * quad + i, o[df][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (quad == 0) {
+          __hip_atomic_store(out + D, m_fin * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(out + D + 1, l_fin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      int before = 0;
+      if (lane == 0) before = __hip_atomic_fetch_add(arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      before = __shfl(before, 0, 64);
+      if (lane == 0) *arrived = before;
+      if (before == w.splits - 1 && lane == 0)
+        __hip_atomic_store(arrivals, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (*arrived != w.splits - 1) return;
+    asm volatile("" ::: "memory");
+    for (int vv = wave; vv < nvec; vv += kThreads / 64)
+      merge_splits<D / 64, true>(a, w.row0 + vv / G, kvh * G + vv % G, w.splits, lane);
+    return;
   }
   if (!v_ok) return;
   const int row = w.row0 + vr, qh = kvh * G + vg;
@@ -701,38 +745,32 @@ __global__ void __launch_bounds__(kThreads) attention_valu_kernel(AttentionArgs 
 
 // ---------------------------------------------------------------- split combine
 
-// One wave per (row, query head), four per block: merge the row's splits, normalise and
-// write the operand. Lane s < splits holds split s's statistics; lane L owns head
-// dimensions L*E .. L*E+E-1 (E = D / 64, at least 1). MFMA-path rows with a single split
-// were written by the attention kernel already.
-// The statistics and the first four splits' vectors are loaded together (unconditionally,
-// at clamped addresses): the kernel is a short latency-bound chain.
-template <int E>
-__global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a, int mfma_path) {
-  const int pair = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (pair >= a.rows * a.q_heads) return;
-  const int r = pair / a.q_heads, qh = pair - r * a.q_heads;
+// Merges the splits of one (row, query head) in split order, normalises and writes the
+// operand; called by a whole wave. Lane s < splits holds split s's statistics; lane L owns
+// head dimensions L*E .. L*E+E-1 (E = D / 64, at least 1). The statistics and the first
+// four splits' vectors are loaded together (unconditionally, at clamped addresses): the
+// merge is a short latency-bound chain. kCoherent: the partials were written by workgroups
+// of this launch, possibly on other XCDs, and are read with device-scope loads (which do not
+// hit a stale line of this XCD's L2); the arithmetic is the same either way.
+template <int E, bool kCoherent>
+__device__ inline void merge_splits(const AttentionArgs& a, int r, int qh, int splits, int lane) {
+  auto ld = [](const float* p) -> float {
+    if constexpr (kCoherent)
+      return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      return *p;
+  };
   const int D = a.head_dim;
-  int splits;
-  if (mfma_path) {
-    splits = uniform_load(a.row_splits + r);
-    if (splits == 1) return;
-  } else {
-    const int ctx = uniform_load(a.row_position + r) + 1;
-    const int per = valu_split_length(ctx, a.max_splits, a.split_unit);
-    splits = (ctx + per - 1) / per;
-  }
   const int stride = D + 2;
   const float* part = partial_at(a, r, qh, 0);
   const int dl = min(lane * E, D - E);  // lanes past D re-read the last elements
   const float* stat = part + (size_t)min(lane, splits - 1) * stride + D;
-  const float ms_raw = stat[0], ls_raw = stat[1];
+  const float ms_raw = ld(stat), ls_raw = ld(stat + 1);
   float pv[4][E];
 #pragma unroll
   for (int u = 0; u < 4; ++u)
 #pragma unroll
-    for (int e = 0; e < E; ++e) pv[u][e] = part[(size_t)min(u, splits - 1) * stride + dl + e];
+    for (int e = 0; e < E; ++e) pv[u][e] = ld(part + (size_t)min(u, splits - 1) * stride + dl + e);
   const float ms = lane < splits ? ms_raw : -INFINITY;
   const float ls = lane < splits ? ls_raw : 0.0f;
   float m = ms;
@@ -752,7 +790,7 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int e = 0; e < E; ++e) pv[u][e] = part[(size_t)min(sp0 + u, splits - 1) * stride + dl + e];
+        for (int e = 0; e < E; ++e) pv[u][e] = ld(part + (size_t)min(sp0 + u, splits - 1) * stride + dl + e);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -779,6 +817,26 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a,
       if (a.out_lo) a.out_lo[at] = 0;
     }
   }
+}
+
+// One wave per (row, query head), four per block: merge_splits of the row's splits.
+// MFMA-path rows with a single split (or merged by the attention kernel) are skipped.
+template <int E>
+__global__ void __launch_bounds__(256) attention_combine_kernel(AttentionArgs a, int mfma_path) {
+  const int pair = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (pair >= a.rows * a.q_heads) return;
+  const int r = pair / a.q_heads, qh = pair - r * a.q_heads;
+  int splits;
+  if (mfma_path) {
+    splits = uniform_load(a.row_splits + r);
+    if (splits == 1) return;
+  } else {
+    const int ctx = uniform_load(a.row_position + r) + 1;
+    const int per = valu_split_length(ctx, a.max_splits, a.split_unit);
+    splits = (ctx + per - 1) / per;
+  }
+  merge_splits<E, false>(a, r, qh, splits, lane);
 }
 
 template <int D>

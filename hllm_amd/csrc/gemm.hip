@@ -1020,12 +1020,13 @@ int launch_dma(hipStream_t stream, GemmArgs a, int prec, int rows_bound, int tar
 // straight from memory (global_load_lds), before the loop: the activations of a decode pass
 // were just written by the previous kernel and miss in this XCD's L2, so one wait for all
 // of them replaces one per chunk, and the waves then run without per-chunk barriers.
-template <int MF, int WAVES, int NFW, int KC, int P, bool PAIR>
+template <int MF, int WAVES, int NFW, int KC, int P, bool PAIR, int PW>
 __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int n_tiles, int whole) {
   constexpr int NT = 64 * WAVES, FR = WAVES * NFW;
   constexpr int CHUNK = MF * KC * 64;  // half8s per staged chunk
   constexpr int PIECES = (CHUNK + NT - 1) / NT;
   static_assert(KC % P == 0, "the ring slot of a k-step must be a compile-time index");
+  static_assert(PW * NFW < 64, "the whole path's weight loads in flight fit the wait count");
   static_assert(!PAIR || (NFW == 2 && WAVES % 2 == 0), "gate/up pairs: two fragment rows per wave");
   extern __shared__ float lds[];
   half8* xs = reinterpret_cast<half8*>(lds);  // [2][MF][KC][64]
@@ -1087,7 +1088,15 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
     for (int j = 0; j < NFW; ++j) rb[slot][j] = __builtin_nontemporal_load(W[j] + (size_t)kt * 64);
   };
   if (!PAIR && whole) {
-    // LDS holds fragment (i, s) of the split at (i * per + s) * 64 half8s.
+    // LDS holds fragment (i, s) of the split at (i * per + s) * 64 half8s. The copies are
+    // issued before the first PW k-steps of weights and waited for alone (loads complete in
+    // issue order), so the weight ring stays in flight across the barrier.
+    half8 rw[PW][NFW];
+    auto load_ww = [&](int slot, int kt) {
+      kt = min(kt, kt_last);
+#pragma unroll
+      for (int j = 0; j < NFW; ++j) rw[slot][j] = __builtin_nontemporal_load(W[j] + (size_t)kt * 64);
+    };
     const uint32_t lds_base = (uint32_t)(size_t)((__attribute__((address_space(3))) float*)lds);
 #pragma unroll
     for (int i = 0; i < MF; ++i)
@@ -1095,32 +1104,32 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_decode_kernel(GemmArgs a, int
         lds_copy16(X + (size_t)i * frag_stride + (size_t)(kt0 + s) * 64, (uint32_t)lane * 16,
                    lds_base + (uint32_t)(i * per + s) * 1024);
 #pragma unroll
-    for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
-    wait_counts<0, 15>();
+    for (int sl = 0; sl < PW; ++sl) load_ww(sl, kt0 + sl);
+    wait_counts<PW * NFW, 15>();
     __syncthreads();
-    for (int s0 = 0; s0 < steps; s0 += P) {
+    for (int s0 = 0; s0 < steps; s0 += PW) {
 #pragma unroll
-      for (int j = 0; j < P; ++j) {
+      for (int j = 0; j < PW; ++j) {
         const int step = s0 + j;
         if (step < steps) {
 #pragma unroll
           for (int i = 0; i < MF; ++i) {
             const half8 x = xs[(i * per + step) * 64 + lane];
 #pragma unroll
-            for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rb[j][n], x, acc[i][n]);
+            for (int n = 0; n < NFW; ++n) acc[i][n] = mfma(rw[j][n], x, acc[i][n]);
           }
         }
-        load_w(j, kt0 + step + P);
+        load_ww(j, kt0 + step + PW);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   } else {
+  // The first chunk's activation loads go out before the weight ring's, so that staging
+  // them waits for them alone.
+  if (chunks > 0) fetch_x(0);
 #pragma unroll
   for (int sl = 0; sl < P; ++sl) load_w(sl, kt0 + sl);
-  if (chunks > 0) {
-    fetch_x(0);
-    store_x(0);
-  }
+  if (chunks > 0) store_x(0);
   __syncthreads();
   for (int c = 0; c < chunks; ++c) {
     if (c + 1 < chunks) fetch_x(c + 1);
@@ -1235,7 +1244,7 @@ int env_int(const char* name, int fallback);
 
 // Launches the decode kernel with `waves` waves per workgroup (4, 8 or 16) and the given
 // K split; returns the number of deferred partials (0: the epilogue has been applied).
-template <int MF, int NFW, int KC, int P, bool PAIR>
+template <int MF, int NFW, int KC, int P, bool PAIR, int PW>
 int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
   const int fr = waves * NFW;
   const int n_tiles = (a.N + 16 * fr - 1) / (16 * fr);
@@ -1263,9 +1272,11 @@ int launch_decode_waves(hipStream_t stream, GemmArgs a, int waves, int ksplit) {
     observed(name, [&] { kernel<<<grid, 64 * waves, lds, stream>>>(a, n_tiles, whole); });
   };
   if (waves >= 8)
-    go(&gemm_decode_kernel<MF, 8, NFW, KC, P, PAIR>, kernel_name<MF, 8, NFW, KC, P, PAIR ? 1 : 0>("gemm_decode_kernel"));
+    go(&gemm_decode_kernel<MF, 8, NFW, KC, P, PAIR, PW>,
+       kernel_name<MF, 8, NFW, KC, P, PAIR ? 1 : 0, PW>("gemm_decode_kernel"));
   else
-    go(&gemm_decode_kernel<MF, 4, NFW, KC, P, PAIR>, kernel_name<MF, 4, NFW, KC, P, PAIR ? 1 : 0>("gemm_decode_kernel"));
+    go(&gemm_decode_kernel<MF, 4, NFW, KC, P, PAIR, PW>,
+       kernel_name<MF, 4, NFW, KC, P, PAIR ? 1 : 0, PW>("gemm_decode_kernel"));
   return ksplit > 1 ? ksplit : 0;
 }
 
@@ -1432,14 +1443,15 @@ int env_int(const char* name, int fallback) {
 // HLLM_ROCM_DECODE_WAVES / _TARGET / _RING / _CHUNK / _FRAGS override the deferred shape,
 // HLLM_ROCM_DECODE_PAIR_WAVES / _PAIR_CHUNK the paired one, for sweeps.
 struct DecodeShape {
-  int waves, target_waves_per_cu, ring, chunk, frags;
+  int waves, target_waves_per_cu, ring, chunk, frags, whole_ring;
 };
 const DecodeShape& decode_shape(bool pair) {
   static const DecodeShape deferred{env_int("HLLM_ROCM_DECODE_WAVES", 8), env_int("HLLM_ROCM_DECODE_TARGET", 6),
                                     env_int("HLLM_ROCM_DECODE_RING", 4), env_int("HLLM_ROCM_DECODE_CHUNK", 4),
-                                    env_int("HLLM_ROCM_DECODE_FRAGS", 1)};
+                                    env_int("HLLM_ROCM_DECODE_FRAGS", 1),
+                                    env_int("HLLM_ROCM_DECODE_WHOLE_RING", 4)};
   static const DecodeShape paired{env_int("HLLM_ROCM_DECODE_PAIR_WAVES", 4), 0, 8,
-                                  env_int("HLLM_ROCM_DECODE_PAIR_CHUNK", 16), 2};
+                                  env_int("HLLM_ROCM_DECODE_PAIR_CHUNK", 16), 2, 8};
   return pair ? paired : deferred;
 }
 
@@ -1463,7 +1475,7 @@ int decode_frags(const GemmArgs& a, int waves) {
   return nfw;
 }
 
-template <int MF, int KC, int P>
+template <int MF, int KC, int P, int PW>
 int launch_decode_variant(hipStream_t stream, const GemmArgs& a, int cus) {
   const bool pair = a.epilogue == kEpiSwiglu;
   const DecodeShape& d = decode_shape(pair);
@@ -1480,18 +1492,22 @@ int launch_decode_variant(hipStream_t stream, const GemmArgs& a, int cus) {
     const int per = (chunks + ksplit - 1) / ksplit;
     ksplit = (chunks + per - 1) / per;
   }
-  if (pair) return launch_decode_waves<MF, 2, KC, P, true>(stream, a, waves, 1);
-  if (nfw == 4) return launch_decode_waves<MF, 4, KC, P, false>(stream, a, waves, ksplit);
-  if (nfw == 2) return launch_decode_waves<MF, 2, KC, P, false>(stream, a, waves, ksplit);
-  return launch_decode_waves<MF, 1, KC, P, false>(stream, a, waves, ksplit);
+  if (pair) return launch_decode_waves<MF, 2, KC, P, true, P>(stream, a, waves, 1);
+  if (nfw == 4) return launch_decode_waves<MF, 4, KC, P, false, (PW > 8 ? 8 : PW)>(stream, a, waves, ksplit);
+  if (nfw == 2) return launch_decode_waves<MF, 2, KC, P, false, PW>(stream, a, waves, ksplit);
+  return launch_decode_waves<MF, 1, KC, P, false, PW>(stream, a, waves, ksplit);
 }
 
 template <int MF>
 int launch_decode_rows(hipStream_t stream, const GemmArgs& a, int cus) {
   const DecodeShape& d = decode_shape(a.epilogue == kEpiSwiglu);
-  if (d.chunk <= 4) return launch_decode_variant<MF, 4, 4>(stream, a, cus);
-  if (d.chunk <= 8) return launch_decode_variant<MF, 8, 8>(stream, a, cus);
-  return launch_decode_variant<MF, 16, 8>(stream, a, cus);
+  if (d.chunk <= 4) {
+    if (d.whole_ring >= 16) return launch_decode_variant<MF, 4, 4, 16>(stream, a, cus);
+    if (d.whole_ring >= 8) return launch_decode_variant<MF, 4, 4, 8>(stream, a, cus);
+    return launch_decode_variant<MF, 4, 4, 4>(stream, a, cus);
+  }
+  if (d.chunk <= 8) return launch_decode_variant<MF, 8, 8, 8>(stream, a, cus);
+  return launch_decode_variant<MF, 16, 8, 8>(stream, a, cus);
 }
 
 int launch_decode(hipStream_t stream, const GemmArgs& a, int rows, int cus) {

@@ -72,6 +72,22 @@ __host__ __device__ inline int attn_item_work(int query_tokens, int first_positi
   attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, count);
   return count[0] + count[1] + count[2];
 }
+// Whether a block of `vectors` query vectors whose keys are split merges its splits in the
+// attention kernel (the last split's workgroup to arrive, decode-like blocks of at most 16
+// vectors) rather than in the combine kernel.
+__host__ __device__ inline bool attn_merges_in_kernel(int vectors, int fold) { return fold && vectors <= 16; }
+// Whether some block of one query item leaves its splits to the combine kernel.
+__host__ __device__ inline bool attn_item_needs_combine(int query_tokens, int first_position, int group,
+                                                        int max_splits, int decode_unit, int fold) {
+  const int qb = attn_block_rows(group);
+  for (int r0 = 0; r0 < query_tokens; r0 += qb) {
+    const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
+    const int keys = first_position + r0 + rows;
+    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
+    if (per < keys && !attn_merges_in_kernel(rows * group, fold)) return true;
+  }
+  return false;
+}
 
 // Where each packed row of a pass comes from, built on the device from ItemMeta.
 struct PackOut {
@@ -90,6 +106,7 @@ struct PackOut {
   int attn_group;          // query heads per KV head
   int attn_max_splits;
   int attn_decode_unit;    // keys per split of decode-like blocks (attn_split_keys)
+  int attn_fold;           // decode-like blocks merge their splits in the attention kernel
 };
 
 // Paged KV pool: [layers][blocks][K, V][kv_heads][...] with keys as [block_tokens][head_dim]
@@ -198,8 +215,10 @@ struct AttentionArgs {
   const AttnWork* work;        // MFMA path work list, its size (device) and the launch's
   const int32_t* work_count;   // workgroups along x, which loop over the list
   int work_grid;
-  int any_split;               // some block's keys are split (MFMA path: the combine runs)
-  const int32_t* row_splits;
+  int any_split;               // some block's splits are left to the combine kernel
+  const int32_t* row_splits;   // [rows] splits the combine kernel merges (1: none)
+  int fold;                    // decode-like blocks merge their splits in the attention kernel
+  int32_t* split_arrivals;     // [rows][kv_heads] arrival counts (zero between launches)
   const int32_t* row_item;
   const int32_t* row_position;
   const ItemMeta* items;

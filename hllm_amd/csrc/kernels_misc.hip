@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
       const int r0 = j / qb * qb, rows = min(qb, (int)it.query_tokens - r0);
       const int keys = (int)it.first_position + r0 + rows;
       const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
-      out.row_splits[r] = (keys + per - 1) / per;
+      out.row_splits[r] = attn_merges_in_kernel(rows * group, out.attn_fold) ? 1 : (keys + per - 1) / per;
     }
   }
   // Attention blocks of this item: query rows [r0, r0 + rows) against keys [0, first + r0 + rows),

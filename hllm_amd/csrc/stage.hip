@@ -316,6 +316,8 @@ class Stage {
   std::set<PassShape> shapes_seen_;
   uint64_t graph_clock_ = 0, graph_captures_ = 0, graph_replays_ = 0;
   DeviceMemory attn_count_;
+  DeviceMemory attn_arrivals_;  // [rows][kv_heads] split arrival counts, zero between launches
+  bool attn_fold_ = true;
 
   // in-flight pass
   bool in_flight_ = false;
@@ -527,6 +529,13 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
     pack_.attn_work = attn_work_.as<AttnWork>();
     attn_count_.allocate(sizeof(int32_t), "attention work");
     pack_.attn_count = attn_count_.as<int32_t>();
+    // Decode-like blocks merge their key splits in the attention kernel (the last split to
+    // arrive) unless HLLM_ROCM_ATTN_FOLD=0 (the combine kernel, for comparisons). The counts
+    // reset themselves, so they are cleared once here.
+    if (const char* v = std::getenv("HLLM_ROCM_ATTN_FOLD")) attn_fold_ = v[0] != '0';
+    attn_arrivals_.allocate(R * K_ * sizeof(int32_t), "attention arrivals");
+    HIP_CHECK(hipMemsetAsync(attn_arrivals_.ptr, 0, attn_arrivals_.bytes, stream_));
+    pack_.attn_fold = attn_fold_ ? 1 : 0;
     pack_.attn_group = (int)group;
     pack_.attn_max_splits = kMaxSplits;
     // Keys per split of decode-like attention blocks; HLLM_ROCM_ATTN_DECODE_SPLIT overrides
@@ -1200,12 +1209,12 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
   // Some block's keys split in two or more: the split combine runs after the attention.
   bool attn_any_split = false;
   if (mfma_attention_) {
-    const int qb = attn_block_rows((int)(Q_ / K_));
     for (uint32_t i = 0; i < n; ++i) {
       const int work = attn_item_work((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
                                       (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit);
       attn_work_count += work;
-      attn_any_split |= work > ((int)pass.item[i].query_tokens + qb - 1) / qb;  // more items than blocks
+      attn_any_split |= attn_item_needs_combine((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
+                                                (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit, pack_.attn_fold);
     }
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
@@ -1305,6 +1314,8 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
       at.work_grid = attn_grid;
       at.any_split = attn_any_split ? 1 : 0;
       at.row_splits = pack_.row_splits;
+      at.fold = pack_.attn_fold;
+      at.split_arrivals = attn_arrivals_.as<int32_t>();
       at.q = q_.as<float>();
       at.rows = R;
       at.q_heads = (int)Q_;

@@ -412,6 +412,49 @@ def test_long_context_split_attention_matches_oracle(execution):
     st.close()
 
 
+def test_in_kernel_split_merge_is_bit_identical_to_the_combine_kernel(monkeypatch):
+    """Decode rows whose key ranges split (up to 3001 keys: seven splits of 512 at most, and
+    several blocks of one pass arriving in any order) merge their splits in the attention
+    kernel: the split's workgroup that arrives last merges them with the combine kernel's
+    arithmetic. With the combine kernel instead (HLLM_ROCM_ATTN_FOLD=0) every pass must give
+    bit-identical logits, tokens and caches, over four passes and two layers (the arrival
+    counts reset themselves between launches), eager and replayed from HIP graphs."""
+    shape = _slice_shape(synthetic.QWEN3_0_6B, 2)
+    lengths = [1, 31, 480, 511, 512, 513, 1024, 1500, 2047, 2048, 3000, 700] * 2
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, shape.vocab, n).tolist() for n in lengths]
+    results = {}
+    for fold in ("1", "0"):
+        _say("split merge, fold", fold)
+        monkeypatch.setenv("HLLM_ROCM_ATTN_FOLD", fold)
+        cfg = model.stage_config(shape, execution="f16", kv_cache_bytes=512 << 20, max_sequences=32,
+                                 max_pass_rows=512, max_seq=4096)
+        st = capi.Stage(cfg)
+        model.synthesize(st, shape, seed=5, norm_sigma=0.1)
+        seqs = [st.allocate(n + 16) for n in lengths]
+        for s, p in zip(seqs, prompts):
+            for pos in range(0, len(p), 512):
+                take = min(512, len(p) - pos)
+                st.execute([capi.item(s, take, pos, sample=pos + take == len(p))], token_ids=p[pos:pos + take])
+        got = []
+        for step in range(8):
+            st.set_graphs(step >= 4)  # passes 4..7 captured and replayed (same shapes as 0..3)
+            items = [capi.item(s, 1, n + step, from_device=True) for s, n in zip(seqs, lengths)]
+            out = st.execute(items, token_ids=[0] * len(seqs), want_logits=step < 4)
+            got.append((np.array(out["tokens"]), out.get("logits")))
+        kv = [st.read_kv(s, layer) for s in seqs[:12] for layer in range(shape.layers)]
+        results[fold] = (got, kv)
+        st.close()
+    (a_out, a_kv), (b_out, b_kv) = results["1"], results["0"]
+    for step, ((ta, la), (tb, lb)) in enumerate(zip(a_out, b_out)):
+        assert np.array_equal(ta, tb), step
+        if la is not None:
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), step
+    for (ka, va), (kb, vb) in zip(a_kv, b_kv):
+        assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32))
+        assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
+
+
 def test_falcon3_slice_head_dim_256_matches_oracle():
     """Falcon3-3B-shaped 1-layer slice (head_dim 256, 12/4 heads, untied head, no QK-norm)."""
     _say("falcon3 slice")
