@@ -38,8 +38,10 @@ constexpr int kAttnPrefillUnit = 1024;
 // `decode_unit` keys (a multiple of 32; 512 by default) for decode-like blocks (at most 16
 // query vectors: the workgroup's four waves share the keys, and short splits balance rows
 // of very different context lengths), every kAttnPrefillUnit keys for prefill blocks.
-__host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits, int decode_unit) {
-  const int unit = vectors <= 16 ? decode_unit : kAttnPrefillUnit;
+__host__ __device__ inline int attn_split_keys(int keys, int vectors, int max_splits, int decode_unit,
+                                               int decode_split) {
+  // Decode-like blocks of more than `decode_unit` keys split every `decode_split` keys.
+  const int unit = vectors > 16 ? kAttnPrefillUnit : keys <= decode_unit ? decode_unit : decode_split;
   int splits = (keys + unit - 1) / unit;
   splits = splits < max_splits ? splits : max_splits;
   const int per = ((keys + splits - 1) / splits + 31) & ~31;
@@ -55,21 +57,21 @@ __host__ __device__ inline int attn_work_class(int per, int vectors, int decode_
 }
 // Work items (block x key split) of one query item, per dispatch class.
 __host__ __device__ inline void attn_item_work_classes(int query_tokens, int first_position, int group,
-                                                       int max_splits, int decode_unit,
+                                                       int max_splits, int decode_unit, int decode_split,
                                                        int (&count)[kAttnClasses]) {
   const int qb = attn_block_rows(group);
   for (int c = 0; c < kAttnClasses; ++c) count[c] = 0;
   for (int r0 = 0; r0 < query_tokens; r0 += qb) {
     const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
     const int keys = first_position + r0 + rows;
-    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
+    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit, decode_split);
     count[attn_work_class(per, rows * group, decode_unit)] += (keys + per - 1) / per;
   }
 }
 __host__ __device__ inline int attn_item_work(int query_tokens, int first_position, int group,
-                                              int max_splits, int decode_unit) {
+                                              int max_splits, int decode_unit, int decode_split) {
   int count[kAttnClasses];
-  attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, count);
+  attn_item_work_classes(query_tokens, first_position, group, max_splits, decode_unit, decode_split, count);
   return count[0] + count[1] + count[2];
 }
 // Whether a block of `vectors` query vectors whose keys are split merges its splits in the
@@ -78,12 +80,13 @@ __host__ __device__ inline int attn_item_work(int query_tokens, int first_positi
 __host__ __device__ inline bool attn_merges_in_kernel(int vectors, int fold) { return fold && vectors <= 16; }
 // Whether some block of one query item leaves its splits to the combine kernel.
 __host__ __device__ inline bool attn_item_needs_combine(int query_tokens, int first_position, int group,
-                                                        int max_splits, int decode_unit, int fold) {
+                                                        int max_splits, int decode_unit, int decode_split,
+                                                        int fold) {
   const int qb = attn_block_rows(group);
   for (int r0 = 0; r0 < query_tokens; r0 += qb) {
     const int rows = query_tokens - r0 < qb ? query_tokens - r0 : qb;
     const int keys = first_position + r0 + rows;
-    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit);
+    const int per = attn_split_keys(keys, rows * group, max_splits, decode_unit, decode_split);
     if (per < keys && !attn_merges_in_kernel(rows * group, fold)) return true;
   }
   return false;
@@ -105,7 +108,8 @@ struct PackOut {
   int32_t* flags;          // [1] the pass's error flags, cleared by the pack kernel
   int attn_group;          // query heads per KV head
   int attn_max_splits;
-  int attn_decode_unit;    // keys per split of decode-like blocks (attn_split_keys)
+  int attn_decode_unit;    // decode-like blocks of at most this many keys are not split
+  int attn_decode_split;   // keys per split of longer decode-like blocks (attn_split_keys)
   int attn_fold;           // decode-like blocks merge their splits in the attention kernel
 };
 

@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
     int c[kAttnClasses] = {0, 0, 0};
     if (out.attn_work)
       attn_item_work_classes((int)items[j].query_tokens, (int)items[j].first_position, out.attn_group,
-                             out.attn_max_splits, out.attn_decode_unit, c);
+                             out.attn_max_splits, out.attn_decode_unit, out.attn_decode_split, c);
     for (int k = 0; k < kAttnClasses; ++k) all[k] += c[k];
     if (j < i) {
       offset += (int)items[j].query_tokens;
@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
       // The key splits of the row's attention block (as the work items below count them).
       const int r0 = j / qb * qb, rows = min(qb, (int)it.query_tokens - r0);
       const int keys = (int)it.first_position + r0 + rows;
-      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
+      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit, out.attn_decode_split);
       out.row_splits[r] = attn_merges_in_kernel(rows * group, out.attn_fold) ? 1 : (keys + per - 1) / per;
     }
   }
@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(kBlock) pack_kernel(const ItemMeta* items, int
       const int r0 = valid ? (nblocks - 1 - k) * qb : 0;
       const int rows = min(qb, q - r0);
       const int keys = first + r0 + rows;
-      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit);
+      const int per = attn_split_keys(keys, rows * group, out.attn_max_splits, out.attn_decode_unit, out.attn_decode_split);
       const int splits = valid ? (keys + per - 1) / per : 0;
       const int cls = attn_work_class(per, rows * group, out.attn_decode_unit);
 #pragma unroll

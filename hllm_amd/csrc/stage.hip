@@ -546,6 +546,12 @@ Stage::Stage(const hllm_rocm_stage_config& c) : c_(c) {
       if (unit < 32 || unit % 32) fail(HLLM_INVALID_REQUEST, "HLLM_ROCM_ATTN_DECODE_SPLIT must be a multiple of 32");
       pack_.attn_decode_unit = unit;
     }
+    pack_.attn_decode_split = pack_.attn_decode_unit;
+    if (const char* v = std::getenv("HLLM_ROCM_ATTN_SPLIT_KEYS")) {
+      const int keys = std::atoi(v);
+      if (keys < 32 || keys % 32) fail(HLLM_INVALID_REQUEST, "HLLM_ROCM_ATTN_SPLIT_KEYS must be a multiple of 32");
+      pack_.attn_decode_split = keys;
+    }
   }
   if (!c.first_stage || !c.final_stage) boundary_dev_.allocate(R * H_ * 2, "boundary");
   pin_items_.allocate(tokens_offset() + R * sizeof(int32_t));
@@ -1211,10 +1217,11 @@ void Stage::submit(const hllm_rocm_pass& pass, bool phases) {
   if (mfma_attention_) {
     for (uint32_t i = 0; i < n; ++i) {
       const int work = attn_item_work((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
-                                      (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit);
+                                      (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit, pack_.attn_decode_split);
       attn_work_count += work;
       attn_any_split |= attn_item_needs_combine((int)pass.item[i].query_tokens, (int)pass.item[i].first_position,
-                                                (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit, pack_.attn_fold);
+                                                (int)(Q_ / K_), kMaxSplits, pack_.attn_decode_unit, pack_.attn_decode_split,
+                                                pack_.attn_fold);
     }
     if ((uint64_t)attn_work_count > attn_work_max_) fail(HLLM_INTERNAL, "attention work list overflow");
   }
