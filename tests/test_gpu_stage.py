@@ -6,6 +6,8 @@ Tolerances: F32 execution 3e-5 and F16 execution 5e-3 on the tiny Transformers f
 Qwen3-shaped slices in F16 execution: max-abs <= 2e-2 and cosine >= 0.9999 against the F32
 CPU oracle; F32 execution (split-precision GEMMs, F32 KV): |d| <= 2e-4 + 1e-4 |expected|.
 """
+from dataclasses import replace
+
 import numpy as np
 import pytest
 
@@ -412,15 +414,25 @@ def test_long_context_split_attention_matches_oracle(execution):
     st.close()
 
 
-def test_in_kernel_split_merge_is_bit_identical_to_the_combine_kernel(monkeypatch):
+SPLIT_MERGE_SHAPES = {
+    "d128-qwen3": (synthetic.with_layers(synthetic.QWEN3_0_6B, 2), 2),
+    "d64-llama": (synthetic.ModelShape("d64-llama", 2, 2048, 8192, 32, 8, 64, 4096, qk_norm=False,
+                                       tied=False), 1),
+    "d256-falcon3": (replace(synthetic.FALCON3_3B, layers=1, vocab=8192), 1),
+}
+
+
+@pytest.mark.parametrize("name", list(SPLIT_MERGE_SHAPES))
+def test_in_kernel_split_merge_is_bit_identical_to_the_combine_kernel(monkeypatch, name):
     """Decode rows whose key ranges split (up to 3001 keys: seven splits of 512 at most, and
     several blocks of one pass arriving in any order) merge their splits in the attention
     kernel: the split's workgroup that arrives last merges them with the combine kernel's
     arithmetic. With the combine kernel instead (HLLM_ROCM_ATTN_FOLD=0) every pass must give
-    bit-identical logits, tokens and caches, over four passes and two layers (the arrival
-    counts reset themselves between launches), eager and replayed from HIP graphs."""
-    shape = _slice_shape(synthetic.QWEN3_0_6B, 2)
-    lengths = [1, 31, 480, 511, 512, 513, 1024, 1500, 2047, 2048, 3000, 700] * 2
+    bit-identical logits, tokens and caches, over four passes and every layer (the arrival
+    counts reset themselves between launches), eager and replayed from HIP graphs, at head
+    dims 128, 64 and 256."""
+    shape, copies = SPLIT_MERGE_SHAPES[name]
+    lengths = [1, 31, 480, 511, 512, 513, 1024, 1500, 2047, 2048, 3000, 700] * copies
     rng = np.random.default_rng(9)
     prompts = [rng.integers(0, shape.vocab, n).tolist() for n in lengths]
     results = {}
