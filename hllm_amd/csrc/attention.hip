@@ -572,7 +572,13 @@ __global__ void __launch_bounds__(kThreads, D <= 128 ? 3 : 1) attention_mfma_ker
     // Wave 0 publishes this split's partial with device-scope stores, waits for them to
     // complete and counts the arrival; the count's last arrival resets it for the next
     // launch and the four waves merge the block's vectors. No cache-wide fence is needed:
-    // every access to the partials and the count is device-coherent on its own.
+    // every access to the partials and the count is a relaxed agent-scope atomic, which
+    // gfx950 performs at the device's coherence point (`sc1` stores write through the
+    // XCD's L2, `sc1` loads do not hit a stale line of it). An agent-scope release fence
+    // would add `buffer_wbl2` (write back the whole L2, for plain stores, of which the
+    // merge reads none) to the `s_waitcnt vmcnt(0)` below, and an acquire fence
+    // `buffer_inv` (for plain loads, of which it issues none); the wait alone orders the
+    // partial's stores before the count, and the merge's loads follow the count's value.
     int32_t* arrivals = a.split_arrivals + (size_t)w.row0 * a.kv_heads + kvh;
     int* arrived = reinterpret_cast<int*>(smem);  // wave 0 has finished reading the merge area
     if (wave == 0) {
