@@ -344,6 +344,44 @@ def test_request_validation_errors():
     last.close()
 
 
+def test_pass_size_limits():
+    """The pass's size limits on the tiny reference stage (8 sequence slots, 64 rows per pass,
+    a 32-position context): an empty pass is INVALID_REQUEST and a pass of 65 rows
+    RESOURCE_EXHAUSTED, with nothing changed; a pass of exactly 64 rows over all 8 slots runs
+    and every item's logits equal the oracle's run of that sequence alone (F32 bounds); a
+    sequence takes its 32nd and last position in a decode pass, and a 33rd is refused."""
+    _say("pass size limits")
+    shape = models.tiny_reference_shape()
+    st = tiny_stage("f32")
+    ost = oracle.OracleStage(models.tiny_reference_stage())
+    rng = np.random.default_rng(5)
+    with pytest.raises(capi.StageError) as e:
+        st.execute([], token_ids=[])
+    assert e.value.status == capi.INVALID_REQUEST
+    seqs = [st.allocate(32) for _ in range(8)]
+    ids = [rng.integers(0, shape.vocab, 9 if i == 0 else 8).tolist() for i in range(8)]
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(s, len(t), 0) for s, t in zip(seqs, ids)], token_ids=sum(ids, []))
+    assert e.value.status == capi.RESOURCE_EXHAUSTED
+    assert all(st.length(s) == 0 for s in seqs)
+    ids[0] = ids[0][:8]
+    out = st.execute([capi.item(s, 8, 0) for s in seqs], token_ids=sum(ids, []), want_logits=True)
+    for i, t in enumerate(ids):
+        o = ost.allocate_sequence(32)
+        tr = []
+        ost.execute(np.array(t, np.uint64), 0, o, tr)
+        assert within(out["logits"][i], tr[-1], "f32"), i
+    # Fill the first sequence to 31 positions, then decode its last position.
+    rest = rng.integers(0, shape.vocab, 23).tolist()
+    st.execute([capi.item(seqs[0], 23, 8, sample=False)], token_ids=rest)
+    out = st.execute([capi.item(seqs[0], 1, 31)], token_ids=[1])
+    assert st.length(seqs[0]) == 32 and int(out["tokens"][0]) < shape.vocab
+    with pytest.raises(capi.StageError) as e:
+        st.execute([capi.item(seqs[0], 1, 32)], token_ids=[1])
+    assert e.value.status == capi.INVALID_REQUEST
+    st.close()
+
+
 def test_weight_validation_errors():
     _say("weight validation")
     shape = models.tiny_reference_shape()
