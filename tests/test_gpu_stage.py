@@ -466,9 +466,9 @@ def test_in_kernel_split_merge_is_bit_identical_to_the_combine_kernel(monkeypatc
     several blocks of one pass arriving in any order) merge their splits in the attention
     kernel: the split's workgroup that arrives last merges them with the combine kernel's
     arithmetic. With the combine kernel instead (HLLM_ROCM_ATTN_FOLD=0) every pass must give
-    bit-identical logits, tokens and caches, over four passes and every layer (the arrival
-    counts reset themselves between launches), eager and replayed from HIP graphs, at head
-    dims 128, 64 and 256."""
+    bit-identical logits, tokens and caches, over eight decode passes and every layer (the
+    arrival counts reset themselves between launches), eager and replayed from HIP graphs,
+    then a mixed pass of short chunks at long positions, at head dims 128, 64 and 256."""
     shape, copies = SPLIT_MERGE_SHAPES[name]
     lengths = [1, 31, 480, 511, 512, 513, 1024, 1500, 2047, 2048, 3000, 700] * copies
     rng = np.random.default_rng(9)
@@ -492,6 +492,15 @@ def test_in_kernel_split_merge_is_bit_identical_to_the_combine_kernel(monkeypatc
             items = [capi.item(s, 1, n + step, from_device=True) for s, n in zip(seqs, lengths)]
             out = st.execute(items, token_ids=[0] * len(seqs), want_logits=step < 4)
             got.append((np.array(out["tokens"]), out.get("logits")))
+        # One mixed pass: short chunks of 2-8 rows at long positions (blocks of at most 16
+        # query vectors merge in the kernel, larger ones in the combine kernel, in one launch)
+        # beside single-token rows.
+        st.set_graphs(False)
+        tails = [(2, 3, 4, 5, 8)[i % 5] if n >= 513 else 1 for i, n in enumerate(lengths)]
+        items = [capi.item(s, q, n + 8) for s, n, q in zip(seqs, lengths, tails)]
+        ids = np.random.default_rng(10).integers(0, shape.vocab, sum(tails)).tolist()
+        out = st.execute(items, token_ids=ids, want_logits=True)
+        got.append((np.array(out["tokens"]), out.get("logits")))
         kv = [st.read_kv(s, layer) for s in seqs[:12] for layer in range(shape.layers)]
         results[fold] = (got, kv)
         st.close()
